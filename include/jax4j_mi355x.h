@@ -1,0 +1,187 @@
+/*
+ * jax4j_mi355x.h -- C ABI of the MI355X (gfx950) GGUF quantized-matmul engine.
+ *
+ * This is the boundary a jax4j tensor backend binds with Java FFM downcalls: plain C types,
+ * status-int returns, opaque 64-bit buffer handles and out-parameters, no C++ or torch
+ * types. Every entry point names the reference interface it serves. Citations are relative
+ * to the jax4j 0.2.1 checkout with these prefixes:
+ *   spi/  = jax4j-core/src/main/java/com/nablatensor/jax4j/tensor/spi/
+ *   core/ = jax4j-core/src/main/java/com/nablatensor/jax4j/
+ *   rocm/ = jax4j-engine-rocm/src/main/java/com/nablatensor/jax4j/backend/rocm/
+ *
+ * Conventions
+ *  - Every function returns J4Q_OK (0) or a J4Q_E* code; on failure j4q_last_error() holds a
+ *    message for the calling thread. The codes map to the reference's exception types:
+ *      J4Q_EINVAL, J4Q_EUNSUPPORTED, J4Q_EHANDLE -> IllegalArgumentException
+ *          (core/backend/cpu/CpuBackend.java:698-701, 712-714, 757-761)
+ *      J4Q_ENODEV                  -> IllegalStateException (core/tensor/BackendRegistry.java:72)
+ *      J4Q_EHIP, J4Q_ENOMEM        -> RuntimeException("<op> failed: <hip message> (code N)")
+ *                                      (rocm/HipRuntime.java:129-141)
+ *  - Arguments are validated on the host before any HIP call, so every error path above is
+ *    reachable without a GPU.
+ *  - All calls are thread-safe (one engine mutex); kernels run in order on one engine stream.
+ *    Functions taking a `stream` argument instead enqueue on the caller's hipStream_t
+ *    (NULL = the engine stream) and return without synchronising.
+ *  - Buffers returned through a j4q_buffer* are owned by the engine until j4q_release.
+ */
+#ifndef JAX4J_MI355X_H
+#define JAX4J_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define J4Q_ABI_VERSION 1
+
+enum j4q_status {
+    J4Q_OK = 0,
+    J4Q_EINVAL = 1,      /* bad shape, size, index or argument */
+    J4Q_EUNSUPPORTED = 2, /* quant type or variant this engine does not implement */
+    J4Q_ENODEV = 3,      /* no usable gfx950 device, or j4q_init not called successfully */
+    J4Q_EHIP = 4,        /* a HIP runtime call failed */
+    J4Q_ENOMEM = 5,      /* device or host allocation failed */
+    J4Q_EHANDLE = 6      /* unknown, released or wrong-kind buffer handle */
+};
+
+/* GGUF type ids, identical to core/tensor/QuantType.java:5-13. */
+enum j4q_quant_type { J4Q_Q4_0 = 2, J4Q_Q8_0 = 8, J4Q_Q4_K = 12, J4Q_Q6_K = 14, J4Q_Q2_0 = 42 };
+
+/* Buffer kinds reported by j4q_buffer_info. */
+enum j4q_kind { J4Q_KIND_QUANT = 1, J4Q_KIND_F32 = 2, J4Q_KIND_BF16 = 3, J4Q_KIND_I8 = 4 };
+
+/* Prefill GEMM variants (engine-local; the SPI has no matmul over quantized weights). */
+enum j4q_gemm_variant { J4Q_GEMM_INT8 = 0, J4Q_GEMM_BF16 = 1 };
+
+typedef uint64_t j4q_buffer; /* 0 is never a valid handle */
+
+typedef struct j4q_device_props {
+    char name[256];
+    char arch[64];          /* e.g. "gfx950:sramecc+:xnack-" */
+    int32_t device;
+    int32_t compute_units;
+    int32_t max_clock_khz;
+    int32_t l2_bytes;
+    uint64_t hbm_bytes;
+} j4q_device_props;
+
+typedef struct j4q_buffer_desc {
+    int32_t kind;           /* j4q_kind */
+    int32_t quant_type;     /* GGUF id for J4Q_KIND_QUANT, else 0 */
+    int32_t rank;           /* 1 or 2 */
+    int32_t reserved;
+    int64_t dims[2];        /* logical shape; quantized: [rows, cols] as in uploadQuantized */
+    uint64_t bytes;         /* device bytes holding the data */
+    void *device_ptr;       /* base of the device allocation */
+} j4q_buffer_desc;
+
+/* ---- lifecycle (rocm/HipRuntime.java:145-228; rocm/RocmBackend.java:433-461) ---------- */
+
+/* ABI version of the loaded library (J4Q_ABI_VERSION). Never fails. */
+int j4q_abi_version(void);
+/* 1 if a gfx950 device is present and usable, else 0. Never fails, never throws
+ * (ComputeBackend.isAvailable, spi/ComputeBackend.java:43; pattern rocm/HipRuntime.java:145-158). */
+int j4q_probe(void);
+/* Selects `device`, creates the engine stream. Idempotent for the same device. */
+int j4q_init(int device);
+/* Message of the last failing call on this thread ("" if none). Never NULL. */
+const char *j4q_last_error(void);
+int j4q_device_info(j4q_device_props *out);
+/* Block until all work queued on the engine stream is done (spi/ComputeBackend.java:277). */
+int j4q_sync(void);
+/* The engine stream as a hipStream_t, for callers that order their own work after it. */
+int j4q_stream(void **out_stream);
+
+/* ---- quant type table (core/tensor/QuantType.java:4-53) -------------------------------- */
+
+/* Block geometry of a GGUF id this engine knows (QuantType rows 5-13). */
+int j4q_quant_type_info(int quant_type, int32_t *block_elements, int32_t *block_bytes);
+/* QuantType.byteSizeFor (QuantType.java:46-53): J4Q_EINVAL if not block-aligned. */
+int j4q_quant_byte_size(int quant_type, int64_t elements, uint64_t *out_bytes);
+/* QuantizedOps.supportedQuantTypes (spi/QuantizedOps.java:21; CPU set at
+ * core/backend/cpu/CpuBackend.java:691-693). Writes up to `capacity` ids, sets *count. */
+int j4q_supported_quant_types(int32_t *ids, int32_t capacity, int32_t *count);
+
+/* ---- buffers (spi/ComputeBackend.java:48, 87, 280; spi/DeviceBuffer.java:26-33) -------- */
+
+/* QuantizedOps.uploadQuantized (spi/QuantizedOps.java:24; CPU copy at CpuBackend.java:696-705).
+ * Copies `nbytes` of GGUF blocks for a [rows, cols] matrix into HBM and repacks them once
+ * into the engine's split layout. Requires cols % blockElements == 0 and
+ * nbytes == rows * cols / blockElements * blockBytes. The caller keeps its memory. */
+int j4q_upload_quantized(int quant_type, const void *blocks, uint64_t nbytes, int64_t rows, int64_t cols,
+                         j4q_buffer *out);
+/* Same, for a GGUF blob already resident in device memory (e.g. a file copied to HBM). */
+int j4q_upload_quantized_device(int quant_type, const void *device_blocks, uint64_t nbytes, int64_t rows,
+                                int64_t cols, j4q_buffer *out);
+/* Writes the matrix back as GGUF blocks (bit-exact inverse of the repack). */
+int j4q_export_quantized(j4q_buffer weights, void *blocks, uint64_t nbytes);
+/* ComputeBackend.upload for F32 data (spi/ComputeBackend.java:48). rank 1 or 2. */
+int j4q_upload_f32(const float *data, int32_t rank, const int64_t *dims, j4q_buffer *out);
+/* bf16 activations for the prefill GEMM (DType has no BF16, core/tensor/DType.java:19-21). */
+int j4q_upload_bf16(const uint16_t *data, int32_t rank, const int64_t *dims, j4q_buffer *out);
+/* ComputeBackend.download (spi/ComputeBackend.java:87): syncs, then copies `count` floats. */
+int j4q_download_f32(j4q_buffer buffer, float *out, int64_t count);
+/* Raw copy of any non-quantized buffer (int8 / bf16 / f32), syncing first. */
+int j4q_download_bytes(j4q_buffer buffer, void *out, uint64_t nbytes);
+int j4q_buffer_info(j4q_buffer buffer, j4q_buffer_desc *out);
+/* ComputeBackend.release (spi/ComputeBackend.java:280). Releasing 0 is a no-op. */
+int j4q_release(j4q_buffer buffer);
+
+/* ---- the quantized ops (spi/QuantizedOps.java:27-33) ----------------------------------- */
+
+/* QuantizedOps.quantMatvec (QuantizedOps.java:27; CpuBackend.java:708-725).
+ * x with exactly cols elements (any rank) -> y F32 [rows]. Engine extension: x of shape
+ * [B, cols] with B > 1 -> y F32 [B, rows] (row b of y is quantMatvec of row b of x). */
+int j4q_quant_matvec(j4q_buffer weights, j4q_buffer x, j4q_buffer *y);
+/* QuantizedOps.quantMatvecAdd (QuantizedOps.java:30; CpuBackend.java:728-736):
+ * y = (W.x) + add, the add rounded separately. add needs at least as many elements as y. */
+int j4q_quant_matvec_add(j4q_buffer weights, j4q_buffer x, j4q_buffer add, j4q_buffer *y);
+/* QuantizedOps.quantGatherRow (QuantizedOps.java:33; CpuBackend.java:739-755): one row
+ * dequantized to F32 [cols], bit-exact. Rows outside [0, rows) -> J4Q_EINVAL. */
+int j4q_quant_gather_row(j4q_buffer weights, int64_t row, j4q_buffer *y);
+/* Whole-matrix dequantization to F32 [rows, cols], bit-exact (engine-local export). */
+int j4q_quant_dequantize(j4q_buffer weights, j4q_buffer *y);
+
+/* ---- prefill GEMM (engine-local; no SPI counterpart, see CpuBackend.java:712) ---------- */
+
+/* bf16 X [M, K] -> int8 per 32-element block with an fp32 scale per block:
+ * s = amax/127, q = clamp(roundf(x * (1/s)), -127, 127) (ggml quantize_row_q8_0, fp32 scale). */
+int j4q_quantize_act(j4q_buffer x_bf16, j4q_buffer *xq_i8, j4q_buffer *scales_f32);
+/* Y F32 [M, N] = X [M, K] . W^T for a Q8_0 W [N, K]. X is bf16 (or F32, rounded to bf16
+ * first). J4Q_GEMM_INT8 quantizes X per 32 and runs int8 MFMA; J4Q_GEMM_BF16 runs bf16
+ * MFMA on W dequantized into LDS. */
+int j4q_quant_matmul(j4q_buffer weights, j4q_buffer x, int variant, j4q_buffer *y);
+
+/* ---- stream-ordered entry points on caller memory (no allocation, no sync) ------------- */
+
+/* quantMatvec / quantMatvecAdd into caller device memory: x_dev [batch, cols] and y_dev
+ * [batch, rows] fp32 (16-byte aligned); add_dev NULL or [batch, rows]. */
+int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *add_dev, float *y_dev,
+                          int64_t batch, void *stream);
+/* Prefill GEMM into caller memory. x_dev bf16 [m, cols]; y_dev fp32 [m, rows]. The int8
+ * variant also needs xq_dev int8 [m, cols] and xs_dev fp32 [m, cols/32] as workspace;
+ * the bf16 variant ignores them. */
+int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, int8_t *xq_dev,
+                          float *xs_dev, float *y_dev, void *stream);
+
+/* ---- seeded synthetic inputs (benchmark support; no reference counterpart) ------------- */
+
+/* GGUF blocks for a [rows, cols] matrix with the benchmark distributions, written to host
+ * memory; bit-identical to the device generator below. */
+int j4q_synth_quant_host(int quant_type, uint64_t seed, int64_t rows, int64_t cols, void *out, uint64_t nbytes);
+int j4q_synth_quant_device(int quant_type, uint64_t seed, int64_t rows, int64_t cols, void *device_out,
+                           uint64_t nbytes, void *stream);
+/* N(0,1) fp32 values, or their round-to-nearest-even bf16. */
+int j4q_synth_f32_host(uint64_t seed, int64_t n, float *out);
+int j4q_synth_bf16_host(uint64_t seed, int64_t n, uint16_t *out);
+int j4q_synth_f32_device(uint64_t seed, int64_t n, float *device_out, void *stream);
+int j4q_synth_bf16_device(uint64_t seed, int64_t n, uint16_t *device_out, void *stream);
+/* Occupies `stream` for `microseconds` (<= 10 s) of device wall-clock time, so a host can
+ * queue many short launches behind it and time them back to back with events. */
+int j4q_spin(uint32_t microseconds, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JAX4J_MI355X_H */

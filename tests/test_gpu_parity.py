@@ -1,0 +1,256 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bars: dequantized weights and layout round trips are bit-exact; GEMV outputs are within
+max|dy| <= 1e-3 * ||y_ref||_inf of the fp64 oracle (and one-hot / known-answer cases are
+exact, since every partial sum there is exactly representable).
+"""
+from __future__ import annotations
+
+import json
+import sys
+import threading
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from jax4j_amd import IllegalArgumentException, QuantType
+from jax4j_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+KAT = json.loads((Path(__file__).parent / "golden" / "kat_blocks.json").read_text())["cases"]
+FORMATS = [QuantType.Q4_0, QuantType.Q8_0, QuantType.Q4_K, QuantType.Q6_K, QuantType.Q2_0]
+TOL = 1e-3
+
+# (rows, cols) per format: small/odd shapes plus the benchmark shapes.
+SHAPES = {
+    QuantType.Q4_0: [(1, 32), (13, 96), (257, 2080), (11008, 4096)],
+    QuantType.Q8_0: [(1, 32), (13, 96), (257, 2080), (4096, 4096)],
+    QuantType.Q4_K: [(1, 256), (13, 768), (257, 2304), (1024, 4096), (14336, 4096)],
+    QuantType.Q6_K: [(1, 256), (13, 768), (257, 2304), (4096, 14336)],
+    QuantType.Q2_0: [(1, 128), (13, 384), (257, 2176), (4096, 4096)],
+}
+CASES = [(qt, r, c) for qt in FORMATS for (r, c) in SHAPES[qt]]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def note(*parts):
+    print("[case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def rel_err(y, y_ref):
+    return float(np.abs(y.astype(np.float64) - y_ref).max() / max(np.abs(y_ref).max(), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def uploaded(backend):
+    """One uploaded matrix per case, shared by the tests of this module."""
+    cache = {}
+
+    def get(qt, rows, cols, seed=0x5EED5):
+        key = (qt, rows, cols, seed)
+        if key not in cache:
+            blob = S.quant_blocks(qt, seed + rows + cols, rows, cols)
+            cache[key] = (blob, backend.upload_quantized(blob, qt, (rows, cols)))
+        return cache[key]
+
+    yield get
+    for _, w in cache.values():
+        backend.release(w)
+
+
+@pytest.mark.parametrize("qt,rows,cols", CASES, ids=lambda v: getattr(v, "name", str(v)))
+def test_export_round_trip_bit_exact(backend, uploaded, qt, rows, cols):
+    note("export", qt.name, rows, cols)
+    blob, w = uploaded(qt, rows, cols)
+    assert np.array_equal(backend.export_quantized(w), blob)
+
+
+@pytest.mark.parametrize("qt,rows,cols", CASES, ids=lambda v: getattr(v, "name", str(v)))
+def test_gather_row_bit_exact(backend, uploaded, qt, rows, cols):
+    note("gather", qt.name, rows, cols)
+    blob, w = uploaded(qt, rows, cols)
+    for r in sorted({0, rows // 2, rows - 1}):
+        y = backend.quant_gather_row(w, r)
+        got = backend.download(y)
+        backend.release(y)
+        assert np.array_equal(bits(got), bits(oracle.gather_row(qt.id, blob, r, rows, cols))), f"row {r}"
+
+
+@pytest.mark.parametrize("qt,rows,cols", [c for c in CASES if c[1] * c[2] <= 1 << 22], ids=lambda v: getattr(v, "name", str(v)))
+def test_dequantize_matrix_bit_exact(backend, uploaded, qt, rows, cols):
+    note("dequantize", qt.name, rows, cols)
+    blob, w = uploaded(qt, rows, cols)
+    y = backend.dequantize(w)
+    got = backend.download(y).reshape(rows, cols)
+    backend.release(y)
+    assert np.array_equal(bits(got), bits(oracle.dequant_matrix(qt.id, blob, rows, cols)))
+
+
+@pytest.mark.parametrize("case", KAT, ids=[c["name"] for c in KAT])
+def test_gemv_known_answers_exact(backend, case):
+    note("kat", case["name"])
+    qt = QuantType.by_id(case["type_id"])
+    blob = np.frombuffer(bytes.fromhex(case["blob_hex"]), dtype=np.uint8)
+    k = case["cols"]
+    w = backend.upload_quantized(blob, qt, (1, k))
+    for x, want in ((np.ones(k, np.float32), case["gemv_x_ones"]), (((np.arange(k) % 7) - 3).astype(np.float32), case["gemv_x_ramp"])):
+        xb = backend.upload(x)
+        y = backend.quant_matvec(w, xb)
+        assert backend.download(y)[0] == np.float32(want)
+        backend.release(y)
+        backend.release(xb)
+    g = backend.quant_gather_row(w, 0)
+    assert np.array_equal(bits(backend.download(g)), bits(np.array(case["values"], np.float32)))
+    backend.release(g)
+    backend.release(w)
+
+
+@pytest.mark.parametrize("qt", FORMATS, ids=lambda q: q.name)
+def test_gemv_one_hot_returns_column_exactly(backend, uploaded, qt):
+    rows, cols = SHAPES[qt][2]
+    note("onehot", qt.name, rows, cols)
+    blob, w = uploaded(qt, rows, cols)
+    wd = oracle.dequant_matrix(qt.id, blob, rows, cols)
+    for j in (0, 31, cols // 2 + 3, cols - 1):
+        x = np.zeros(cols, np.float32)
+        x[j] = 1.0
+        xb = backend.upload(x)
+        y = backend.quant_matvec(w, xb)
+        assert np.array_equal(bits(backend.download(y)), bits(wd[:, j])), f"column {j}"
+        backend.release(y)
+        backend.release(xb)
+
+
+@pytest.mark.parametrize("qt,rows,cols", CASES, ids=lambda v: getattr(v, "name", str(v)))
+def test_gemv_matches_oracle(backend, uploaded, qt, rows, cols):
+    note("gemv", qt.name, rows, cols)
+    blob, w = uploaded(qt, rows, cols)
+    x = S.activations_f32(rows * 31 + cols, cols)
+    xb = backend.upload(x)
+    y = backend.quant_matvec(w, xb)
+    got = backend.download(y)
+    assert got.shape == (rows,)
+    y64 = oracle.matvec_f64(qt.id, blob, rows, cols, x)
+    assert rel_err(got, y64) <= TOL
+    # the engine's fp32 accumulation is far tighter than the bar; a layout or scale bug is not
+    assert rel_err(got, y64) <= 1e-5
+    yref = oracle.matvec(qt.id, blob, rows, cols, x)  # the reference's float loop
+    assert rel_err(got, yref.astype(np.float64)) <= TOL
+    # linearity: scaling x by 2 scales every product and partial sum exactly
+    x2 = backend.upload(2.0 * x)
+    y2 = backend.quant_matvec(w, x2)
+    assert np.array_equal(bits(backend.download(y2)), bits(2.0 * got))
+    for b in (xb, y, x2, y2):
+        backend.release(b)
+
+
+@pytest.mark.parametrize("qt", FORMATS, ids=lambda q: q.name)
+def test_gemv_add_and_batch(backend, uploaded, qt):
+    rows, cols = SHAPES[qt][2]
+    note("add+batch", qt.name, rows, cols)
+    blob, w = uploaded(qt, rows, cols)
+    B = 3
+    xs = S.activations_f32(99, B * cols).reshape(B, cols)
+    add = S.activations_f32(98, rows)
+    singles = []
+    for b in range(B):
+        xb = backend.upload(xs[b])
+        y = backend.quant_matvec(w, xb)
+        singles.append(backend.download(y))
+        backend.release(y)
+        # quantMatvecAdd: y = fl(W.x) + add, the add rounded on its own
+        ab = backend.upload(add)
+        ya = backend.quant_matvec_add(w, xb, ab)
+        assert np.array_equal(bits(backend.download(ya)), bits(singles[-1] + add))
+        for h in (ab, ya, xb):
+            backend.release(h)
+    xbb = backend.upload(xs, shape=(B, cols))
+    yb = backend.quant_matvec(w, xbb)
+    assert yb.shape == (B, rows)
+    got = backend.download(yb).reshape(B, rows)
+    assert np.array_equal(bits(got), bits(np.stack(singles)))
+    backend.release(yb)
+    backend.release(xbb)
+
+
+def test_shape_and_index_errors(backend, uploaded):
+    blob, w = uploaded(QuantType.Q4_0, 13, 96)
+    bad = backend.upload(np.zeros(95, np.float32))
+    with pytest.raises(IllegalArgumentException, match="shape mismatch"):
+        backend.quant_matvec(w, bad)
+    backend.release(bad)
+    with pytest.raises(IllegalArgumentException, match="out of range"):
+        backend.quant_gather_row(w, 13)
+    with pytest.raises(IllegalArgumentException, match="out of range"):
+        backend.quant_gather_row(w, -1)
+    x = backend.upload(np.zeros(96, np.float32))
+    short = backend.upload(np.zeros(12, np.float32))
+    with pytest.raises(IllegalArgumentException, match="add"):
+        backend.quant_matvec_add(w, x, short)
+    backend.release(x)
+    backend.release(short)
+
+
+def test_device_generator_matches_host(backend):
+    import ctypes as C
+
+    from jax4j_amd import _native as N
+
+    lib = N.load()
+    for qt, rows, cols in ((QuantType.Q4_K, 7, 512), (QuantType.Q6_K, 5, 768), (QuantType.Q8_0, 9, 96), (QuantType.Q4_0, 3, 64)):
+        note("synth", qt.name)
+        nbytes = qt.byte_size_for(rows * cols)
+        host = S.quant_blocks(qt, 1234, rows, cols)
+        buf = backend.upload(np.zeros((nbytes + 3) // 4, np.float32))
+        ptr = backend.buffer_desc(buf).device_ptr
+        assert lib.j4q_synth_quant_device(qt.id, 1234, rows, cols, C.c_void_p(ptr), nbytes, None) == 0
+        backend.sync()
+        dev = backend.download(buf).view(np.uint8)[:nbytes]
+        assert np.array_equal(dev, host)
+        backend.release(buf)
+    n = 4099
+    buf = backend.upload(np.zeros(n, np.float32))
+    assert lib.j4q_synth_f32_device(77, n, C.c_void_p(backend.buffer_desc(buf).device_ptr), None) == 0
+    assert np.array_equal(bits(backend.download(buf)), bits(S.activations_f32(77, n)))
+    backend.release(buf)
+
+
+def test_concurrent_callers_get_serial_results(backend, uploaded):
+    """The ABI is callable from many threads (pattern: VulkanExecutionTest.java:72-105)."""
+    blob, w = uploaded(QuantType.Q4_K, 1024, 4096)
+    xs = [S.activations_f32(500 + i, 4096) for i in range(8)]
+    serial = []
+    for x in xs:
+        xb = backend.upload(x)
+        y = backend.quant_matvec(w, xb)
+        serial.append(backend.download(y))
+        backend.release(y)
+        backend.release(xb)
+    results = [None] * len(xs)
+    errors = []
+
+    def work(i):
+        try:
+            xb = backend.upload(xs[i])
+            y = backend.quant_matvec(w, xb)
+            results[i] = backend.download(y)
+            backend.release(y)
+            backend.release(xb)
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(len(xs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors
+    for a, b in zip(results, serial):
+        assert np.array_equal(bits(a), bits(b))
