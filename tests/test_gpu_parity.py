@@ -123,7 +123,11 @@ def test_gemv_one_hot_returns_column_exactly(backend, uploaded, qt):
         x[j] = 1.0
         xb = backend.upload(x)
         y = backend.quant_matvec(w, xb)
-        assert np.array_equal(bits(backend.download(y)), bits(wd[:, j])), f"column {j}"
+        got = backend.download(y)
+        # the column itself (values; a -0.0 weight sums to +0.0 from the +0.0 start) and,
+        # bit for bit, the reference loop's result (float sum = 0.0f; CpuQ4Gemm.java:30)
+        assert np.array_equal(got, wd[:, j]), f"column {j}"
+        assert np.array_equal(bits(got), bits(oracle.matvec(qt.id, blob, rows, cols, x))), f"column {j}"
         backend.release(y)
         backend.release(xb)
 

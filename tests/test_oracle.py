@@ -134,7 +134,9 @@ def test_onehot_x_returns_column_exactly(qt):
     for j in (0, 1, 17, cols // 2 + 5, cols - 1):
         x = np.zeros(cols, dtype=np.float32)
         x[j] = 1.0
-        assert np.array_equal(bits(oracle.matvec(qt.id, blob, rows, cols, x)), bits(w[:, j]))
+        y = oracle.matvec(qt.id, blob, rows, cols, x)
+        assert np.array_equal(y, w[:, j])  # values: a -0.0 weight sums to +0.0
+        assert np.array_equal(bits(y), bits(w[:, j] + np.float32(0.0)))
 
 
 @pytest.mark.parametrize("qt", FORMATS, ids=lambda q: q.name)
