@@ -15,6 +15,7 @@
 
 namespace j4q {
 int64_t gemv_max_cols();
+void gemv_set_cus(int cus);
 }
 
 namespace {
@@ -88,6 +89,7 @@ int init_locked(int device) {
     if (!is_gfx950(p)) return fail(J4Q_ENODEV, "device %d is %s; this engine is built for gfx950 only", device, p.gcnArchName);
     HIP_TRY("hipSetDevice", hipSetDevice(device));
     HIP_TRY("hipStreamCreateWithFlags", hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    j4q::gemv_set_cus(p.multiProcessorCount);
     g_dev = device;
     g_ready = true;
     return J4Q_OK;
@@ -165,6 +167,16 @@ int check_quant_args(int qt, uint64_t nbytes, int64_t rows, int64_t cols, Geomet
     return J4Q_OK;
 }
 
+// The kernels address each section of a resident matrix with 32-bit buffer offsets.
+int check_sections(int qt, int64_t rows, int64_t cols) {
+    const j4q::SplitLayout L = j4q::split_layout(qt, rows, cols);
+    const uint64_t lim = 0x7fffffffull;
+    if (L.qs_bytes > lim || L.qh_bytes > lim || L.sc_bytes > lim || L.d_bytes > lim || rows > (1 << 30))
+        return fail(J4Q_EUNSUPPORTED, "quantized matrix [%lld, %lld] exceeds 2 GiB per section", (long long)rows,
+                    (long long)cols);
+    return J4Q_OK;
+}
+
 int upload_quant_common(int qt, const void *src, bool src_on_device, uint64_t nbytes, int64_t rows, int64_t cols,
                         j4q_buffer *out) {
     Geometry g;
@@ -172,6 +184,7 @@ int upload_quant_common(int qt, const void *src, bool src_on_device, uint64_t nb
     if (!out) return fail(J4Q_EINVAL, "uploadQuantized: out is NULL");
     int rc = check_quant_args(qt, nbytes, rows, cols, &g);
     if (rc) return rc;
+    if ((rc = check_sections(qt, rows, cols))) return rc;
     std::lock_guard<std::mutex> lk(g_mu);
     if ((rc = ensure_ready())) return rc;
     const j4q::SplitLayout L = j4q::split_layout(qt, rows, cols);
