@@ -344,8 +344,7 @@ int ref_gemm_q8_int8_emulated(const int8_t *xq, const float *xs, const uint8_t *
                 int32_t dot = 0;
                 for (int t = 0; t < 32; t++) dot += (int32_t)xb[t] * (int32_t)(int8_t)wb[2 + t];
                 const float s = xs[i * nb + b] * half_at(wb);
-                const float t = s * (float)dot;
-                acc = acc + t;
+                acc = fmaf((float)dot, s, acc);
             }
             y[i * n + j] = acc;
         }

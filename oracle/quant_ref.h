@@ -64,8 +64,9 @@ float ref_bf16_to_f32(uint16_t h);
  * Mirrors ggml quantize_row_q8_0 with the scale kept in fp32. x is bf16 [m, k]. */
 int ref_quantize_act(const uint16_t *x_bf16, int64_t m, int64_t k, int8_t *q, float *scales);
 
-/* Emulated int8 GEMM: Y[i,j] = sum_b (sx[i,b]*dw[j,b]) * (float)(sum_{k in b} qx*qw),
- * blocks summed in order in float. W is Q8_0 [n, k]. The tight check for the int8 path. */
+/* Emulated int8 GEMM: for each block b in order, acc = fmaf((float)dot_b, sx[i,b]*dw[j,b], acc)
+ * with dot_b = sum_{k in b} qx*qw exact in int32 and the scale product rounded to fp32.
+ * W is Q8_0 [n, k]. The tight (bit-exact) check for the int8 path. */
 int ref_gemm_q8_int8_emulated(const int8_t *xq, const float *xs, const uint8_t *w_blob,
                               int64_t m, int64_t n, int64_t k, float *y);
 /* Exact reference for both GEMM variants: Y = X_bf16 . dequant(W)^T in double. */

@@ -1,0 +1,154 @@
+"""GPU parity of the prefill GEMM (Q8_0 weights x bf16 activations) and the activation
+quantizer against the CPU oracle, through the C ABI.
+
+Bars: the quantizer is bit-exact; the int8 variant is bit-identical to the oracle's
+emulation of the int8 arithmetic (exact int32 block dots folded in block order with one
+fp32 FMA each) and within 1e-2 * ||y||inf of the exact product of the bf16 activations
+and the exact dequantized weights; the bf16 variant is within 2e-5 * ||y||inf of the exact
+product with bf16-rounded weights (only fp32 accumulation order differs) and within 1e-2
+of the exact product.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from jax4j_amd import DType, IllegalArgumentException, QuantType
+from jax4j_amd import _native as N
+from jax4j_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16X = 1e-2  # bf16-activation configs
+TOL_ACCUM = 2e-5  # fp32 accumulation-order difference only
+
+# (M, N, K): tails in every dimension, one K block, the benchmark K, M above one tile
+SHAPES = [(1, 32, 32), (5, 13, 256), (33, 96, 512), (128, 128, 128), (130, 257, 1024), (64, 384, 4096)]
+
+
+def note(*parts):
+    print("[case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def rel_err(y, ref):
+    return float(np.abs(y.astype(np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def upload_case(backend, m, n, k, seed):
+    w_blob = S.quant_blocks(QuantType.Q8_0, seed, n, k)
+    xb = S.activations_bf16(seed + 1, m * k).reshape(m, k)
+    w = backend.upload_quantized(w_blob, QuantType.Q8_0, (n, k))
+    x = backend.upload(xb, shape=(m, k), dtype=DType.BF16)
+    return w_blob, xb, w, x
+
+
+@pytest.mark.parametrize("m,k", [(1, 32), (5, 256), (128, 4096), (3, 14336)])
+def test_quantize_act_bit_exact(backend, m, k):
+    note("quantize_act", m, k)
+    xb = S.activations_bf16(7 + m, m * k).reshape(m, k)
+    xb[0, :32] = 0  # an all-zero block: scale 0, quants 0
+    x = backend.upload(xb, shape=(m, k), dtype=DType.BF16)
+    qh, sh = backend.quantize_act(x)
+    q = backend.download_raw(qh).reshape(m, k)
+    s = backend.download(sh).reshape(m, k // 32)
+    q_ref, s_ref = oracle.quantize_act(xb, m, k)
+    assert np.array_equal(q, q_ref)
+    assert np.array_equal(bits(s), bits(s_ref))
+    for h in (x, qh, sh):
+        backend.release(h)
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_gemm_int8_matches_emulation_bit_exact(backend, m, n, k):
+    note("gemm int8", m, n, k)
+    w_blob, xb, w, x = upload_case(backend, m, n, k, 1000 + m + n + k)
+    y = backend.quant_matmul(w, x, "int8")
+    assert y.shape == (m, n)
+    got = backend.download(y).reshape(m, n)
+    xq, xs = oracle.quantize_act(xb, m, k)
+    emu = oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k)
+    assert np.array_equal(bits(got), bits(emu))
+    assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k)) <= TOL_BF16X
+    for h in (w, x, y):
+        backend.release(h)
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_gemm_bf16_matches_reference(backend, m, n, k):
+    note("gemm bf16", m, n, k)
+    w_blob, xb, w, x = upload_case(backend, m, n, k, 2000 + m + n + k)
+    y = backend.quant_matmul(w, x, "bf16")
+    got = backend.download(y).reshape(m, n)
+    assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k, bf16_weights=True)) <= TOL_ACCUM
+    assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k)) <= TOL_BF16X
+    for h in (w, x, y):
+        backend.release(h)
+
+
+def test_gemm_full_size_rows_and_variants_agree(backend):
+    """configs[3] at full size (M=512, N=K=4096): sampled rows against the oracle, and the
+    two variants against each other."""
+    m, n, k = 512, 4096, 4096
+    note("gemm full", m, n, k)
+    w_blob, xb, w, x = upload_case(backend, m, n, k, 0x5EED8)
+    yi = backend.quant_matmul(w, x, "int8")
+    yb = backend.quant_matmul(w, x, "bf16")
+    gi = backend.download(yi).reshape(m, n)
+    gb = backend.download(yb).reshape(m, n)
+    rows = [0, 1, 255, 510, 511]
+    sub = np.ascontiguousarray(xb[rows])
+    y64 = oracle.gemm_f64(sub, w_blob, len(rows), n, k)
+    assert rel_err(gi[rows], y64) <= TOL_BF16X
+    assert rel_err(gb[rows], y64) <= TOL_BF16X
+    xq, xs = oracle.quantize_act(sub, len(rows), k)
+    assert np.array_equal(bits(gi[rows]), bits(oracle.gemm_int8_emulated(xq, xs, w_blob, len(rows), n, k)))
+    assert rel_err(gb[rows], oracle.gemm_f64(sub, w_blob, len(rows), n, k, bf16_weights=True)) <= TOL_ACCUM
+    assert rel_err(gi, gb.astype(np.float64)) <= 2 * TOL_BF16X
+    for h in (w, x, yi, yb):
+        backend.release(h)
+
+
+def test_gemm_into_caller_memory_matches(backend):
+    """j4q_quant_matmul_into on engine-owned device memory gives the allocating call's result."""
+    m, n, k = 70, 160, 512
+    note("gemm into", m, n, k)
+    w_blob, xb, w, x = upload_case(backend, m, n, k, 77)
+    lib = N.load()
+    for variant in ("int8", "bf16"):
+        y_ref = backend.download(backend.quant_matmul(w, x, variant)).reshape(m, n)
+        yb = backend.upload(np.zeros((m, n), np.float32))
+        xq = backend.upload(np.zeros((m, k), np.float32))  # large enough for int8 [m, k]
+        xs = backend.upload(np.zeros((m, k // 32), np.float32))
+        ptr = lambda h: backend.buffer_desc(h).device_ptr
+        v = N.GEMM_INT8 if variant == "int8" else N.GEMM_BF16
+        rc = lib.j4q_quant_matmul_into(w.handle, C.c_void_p(ptr(x)), m, v, C.c_void_p(ptr(xq)), C.c_void_p(ptr(xs)), C.c_void_p(ptr(yb)), None)
+        assert rc == N.J4Q_OK, N.last_error()
+        backend.sync()
+        assert np.array_equal(bits(backend.download(yb).reshape(m, n)), bits(y_ref))
+        for h in (yb, xq, xs):
+            backend.release(h)
+    backend.release(w)
+    backend.release(x)
+
+
+def test_gemm_errors(backend):
+    w4 = backend.upload_quantized(S.quant_blocks(QuantType.Q4_0, 3, 8, 64), QuantType.Q4_0, (8, 64))
+    x = backend.upload(S.activations_bf16(4, 2 * 64).reshape(2, 64), shape=(2, 64), dtype=DType.BF16)
+    with pytest.raises(IllegalArgumentException, match="only Q8_0"):
+        backend.quant_matmul(w4, x, "int8")
+    w8 = backend.upload_quantized(S.quant_blocks(QuantType.Q8_0, 3, 8, 96), QuantType.Q8_0, (8, 96))
+    with pytest.raises(IllegalArgumentException, match="shape mismatch"):
+        backend.quant_matmul(w8, x, "bf16")
+    with pytest.raises(IllegalArgumentException, match="variant"):
+        backend.quant_matmul(w8, x, "fp8")
+    for h in (w4, x, w8):
+        backend.release(h)

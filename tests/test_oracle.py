@@ -10,6 +10,7 @@ and the reference's sequential accumulation order for Q4_0 (CpuQ4Gemm.java:29-45
 from __future__ import annotations
 
 import json
+from fractions import Fraction
 from pathlib import Path
 
 import numpy as np
@@ -231,8 +232,15 @@ def test_gemm_references_against_exact_integer_arithmetic():
     wd = _f16(blk[:, :, 0:2]).reshape(n, nb)
     dots = np.einsum("mbk,nbk->mnb", xq.astype(np.int64).reshape(m, nb, 32), wq)
     scale = (xs[:, None, :] * wd[None, :, :]).astype(np.float32)
-    terms = (scale * dots.astype(np.float32)).astype(np.float32)
-    want = np.add.accumulate(terms, axis=2, dtype=np.float32)[:, :, -1]
+    # acc = fma(dot, s, acc) per block in order: the product and sum are formed exactly
+    # (rationals) and rounded once to float32, ties to even
+    want = np.zeros((m, n), np.float32)
+    for i in range(m):
+        for j in range(n):
+            acc = np.float32(0.0)
+            for b in range(nb):
+                acc = _f32_rne(Fraction(int(dots[i, j, b])) * Fraction(float(scale[i, j, b])) + Fraction(float(acc)))
+            want[i, j] = acc
     got = oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k)
     assert np.array_equal(bits(got), bits(want))
 
@@ -242,6 +250,16 @@ def test_gemm_references_against_exact_integer_arithmetic():
     assert np.allclose(y64, xf @ wdq.T, rtol=1e-12, atol=1e-12)
     wbf = (_round_bf16(wdq.astype(np.float32)).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
     assert np.allclose(oracle.gemm_f64(xb, w_blob, m, n, k, bf16_weights=True), xf @ wbf.T, rtol=1e-12, atol=1e-12)
+
+
+def _f32_rne(fr: Fraction) -> np.float32:
+    """The float32 nearest to the rational `fr`, ties to even (a correctly rounded fp32 op)."""
+    if fr == 0:
+        return np.float32(0.0)
+    a = np.float32(float(fr))
+    cands = [np.nextafter(a, np.float32(-np.inf)), a, np.nextafter(a, np.float32(np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - fr), int(np.float32(c).view(np.uint32)) & 1))
+    return np.float32(best)
 
 
 def _round_bf16(f: np.ndarray) -> np.ndarray:
