@@ -239,6 +239,55 @@ def decode_workload(eng: Engine, batch: int, steps: int, warmup: int, layers: in
     }
 
 
+def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n: int = 4096, k: int = 4096):
+    """Q8_0 prefill GEMM Y[m, n] = X[m, k] . W^T with bf16 X; the int8 variant's
+    timed call includes quantizing X (j4q_quant_matmul_into runs both kernels)."""
+    qt = QuantType.Q8_0
+    blob_bytes = qt.byte_size_for(n * k)
+    copies = max(1, math.ceil(ROTATE_BYTES / blob_bytes))
+    ws = [eng.weights(qt, n, k, 0x5EED8 + 31 * i)[0] for i in range(copies)]
+    x = eng.bf16(m * k, 0x5EED9)
+    xq = eng.hip.malloc(m * k)
+    xs = eng.hip.malloc(4 * m * (k // 32))
+    y = eng.hip.malloc(4 * m * n)
+    handles = [w.handle for w in ws]
+    fn = eng.lib.j4q_quant_matmul_into
+    v = N.GEMM_INT8 if variant == "int8" else N.GEMM_BF16
+    s = C.c_void_p(eng.stream)
+    xp, xqp, xsp, yp = C.c_void_p(x), C.c_void_p(xq), C.c_void_p(xs), C.c_void_p(y)
+
+    def enqueue(i):
+        rc = fn(handles[i % copies], xp, m, v, xqp, xsp, yp, s)
+        if rc:
+            check(rc, "gemm")
+
+    _, host_us, _ = eng.time_region(enqueue, warmup)
+    ms, _, host_bound = eng.time_region(enqueue, steps, host_us)
+    per = ms / steps
+    ops = 2.0 * m * n * k
+    tops = ops / (per * 1e-3) / 1e12
+    peak = INT8_PEAK_TOPS if variant == "int8" else BF16_PEAK_TFLOPS
+    for w in ws:
+        eng.be.release(w)
+    for p in (x, xq, xs, y):
+        eng.hip.free(p)
+    log(f"gemm {variant} M={m}: {per * 1e3:.2f} us, {tops:.0f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% of int8 peak, "
+        f"{100 * tops / peak:.1f}% of {variant} peak)")
+    return {
+        "workload": f"q8_0_gemm_{variant}_m{m}",
+        "variant": variant,
+        "M": m,
+        "N": n,
+        "K": k,
+        "weight_copies": copies,
+        "us_per_call": round(per * 1e3, 3),
+        "TOPS": round(tops, 1),
+        "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+        "frac_variant_peak": round(tops / peak, 4),
+        "host_bound": host_bound,
+    }
+
+
 def cpu_baseline(seconds: float = 10.0):
     """The reference's CPU algorithm (CpuQ4Gemm.multiply, restated in C by the oracle) on the
     headline workload, single-threaded on one pinned host core."""
@@ -294,6 +343,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline workload only, no CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="", help="comma list of workload groups to run: gemv,gemm,decode (default all)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -309,16 +359,23 @@ def main():
 
     head = gemv_workload(eng, "q4_0_gemv_b1", QuantType.Q4_0, 11008, 4096, 1, args.steps, args.warmup)
     others = []
+    groups = set(filter(None, args.only.split(","))) or {"gemv", "gemm", "decode"}
     if not args.quick:
-        others.append(gemv_workload(eng, "q4_0_gemv_b8", QuantType.Q4_0, 11008, 4096, 8, args.steps, args.warmup))
-        others.append(gemv_workload(eng, "q8_0_gemv_b1", QuantType.Q8_0, 4096, 4096, 1, args.steps, args.warmup))
-        others.append(gemv_workload(eng, "q4_k_gemv_gate_up", QuantType.Q4_K, 14336, 4096, 1, args.steps, args.warmup))
-        others.append(gemv_workload(eng, "q6_k_gemv_down", QuantType.Q6_K, 4096, 14336, 1, args.steps, args.warmup))
-        dsteps = max(2, min(20, args.steps // 10))
-        others.append(decode_workload(eng, 1, dsteps, 2))
-        others.append(decode_workload(eng, 16, max(2, dsteps // 4), 1))
+        if "gemv" in groups:
+            others.append(gemv_workload(eng, "q4_0_gemv_b8", QuantType.Q4_0, 11008, 4096, 8, args.steps, args.warmup))
+            others.append(gemv_workload(eng, "q8_0_gemv_b1", QuantType.Q8_0, 4096, 4096, 1, args.steps, args.warmup))
+            others.append(gemv_workload(eng, "q4_k_gemv_gate_up", QuantType.Q4_K, 14336, 4096, 1, args.steps, args.warmup))
+            others.append(gemv_workload(eng, "q6_k_gemv_down", QuantType.Q6_K, 4096, 14336, 1, args.steps, args.warmup))
+        if "gemm" in groups:
+            for m in (32, 128, 512, 2048):
+                for variant in ("int8", "bf16"):
+                    others.append(gemm_workload(eng, m, variant, max(10, args.steps // 2), max(5, args.warmup // 2)))
+        if "decode" in groups:
+            dsteps = max(2, min(20, args.steps // 10))
+            others.append(decode_workload(eng, 1, dsteps, 2))
+            others.append(decode_workload(eng, 16, max(2, dsteps // 4), 1))
 
-    cpu = None if args.quick else cpu_baseline(args.cpu_seconds)
+    cpu = None if (args.quick or args.only) else cpu_baseline(args.cpu_seconds)
     per_ms = head["us_per_launch"] / 1e3
     achieved = head["GBps"]
     out = {

@@ -82,12 +82,17 @@ quantize_act_kernel(const uint16_t *__restrict__ x, int64_t m, int64_t k, int8_t
 __device__ __forceinline__ int mfma_row(int lane, int v) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
 // ---- int8 variant --------------------------------------------------------------------------
-// grid (ceil(N / BN), ceil(M / BM)), 256 threads. Requires K % 32 == 0.
+// grid (ceil(N / BN), ceil(M / BM)), 256 threads. Requires K % 32 == 0. The next stage's
+// global loads are issued into registers before the current stage is computed.
 template <int BM, int BN, int KB>
 __global__ void __launch_bounds__(256)
 gemm_i8_kernel(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs, float *__restrict__ y, int M) {
     constexpr int ROWB = KB * 32 + 16;
     constexpr int TM = BM / 64, TN = BN / 64;  // 32 x 32 tiles per wave
+    constexpr int PIECES = (BM + BN) * KB * 2;  // 16-byte pieces per stage
+    constexpr int PT = (PIECES + 255) / 256;
+    constexpr int SC = (BM + BN) * KB;  // scales per stage
+    constexpr int ST = (SC + 255) / 256;
     __shared__ __attribute__((aligned(16))) int8_t As[BM * ROWB];
     __shared__ __attribute__((aligned(16))) int8_t Bs[BN * ROWB];
     __shared__ __attribute__((aligned(16))) float Sx[KB][BM];
@@ -99,6 +104,55 @@ gemm_i8_kernel(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ 
     const int wm = wave >> 1, wn = wave & 1;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(xq, (uint64_t)M * K);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(w.qs, (uint64_t)N * K);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(xs, (uint64_t)M * nblk * 4);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(w.sc, (uint64_t)N * nblk * 2);
+
+    u32x4 pv[PT];
+    uint32_t sv[ST];
+    auto load_stage = [&](int kb0) {
+#pragma unroll
+        for (int t = 0; t < PT; t++) {
+            const int p = tid + 256 * t;
+            const bool isb = p >= BM * KB * 2;
+            const int pp = isb ? p - BM * KB * 2 : p;
+            const int r = pp / (KB * 2), piece = pp % (KB * 2);
+            const int kbyte = kb0 * 32 + piece * 16;
+            const int grow = (isb ? n0 : m0) + r;
+            const bool ok = p < PIECES && grow < (isb ? N : M) && kbyte < K;
+            pv[t] = ld128(isb ? rb : ra, ok ? (uint32_t)grow * (uint32_t)K + (uint32_t)kbyte : kOob);
+        }
+#pragma unroll
+        for (int t = 0; t < ST; t++) {
+            const int p = tid + 256 * t;
+            if (p < BM * KB) {
+                const int gm = m0 + p / KB, blk = kb0 + p % KB;
+                const bool ok = gm < M && blk < nblk;
+                sv[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? ((uint32_t)gm * nblk + blk) * 4u : kOob, 0, 0);
+            } else {
+                const int pp = p - BM * KB, gn = n0 + pp / KB, blk = kb0 + pp % KB;
+                const bool ok = p < SC && gn < N && blk < nblk;
+                sv[t] = __builtin_amdgcn_raw_buffer_load_b16(rd, ok ? ((uint32_t)gn * nblk + blk) * 2u : kOob, 0, 0);
+            }
+        }
+    };
+    auto store_stage = [&]() {
+#pragma unroll
+        for (int t = 0; t < PT; t++) {
+            const int p = tid + 256 * t;
+            if (p < PIECES) {
+                const bool isb = p >= BM * KB * 2;
+                const int pp = isb ? p - BM * KB * 2 : p;
+                const int r = pp / (KB * 2), piece = pp % (KB * 2);
+                *reinterpret_cast<u32x4 *>((isb ? Bs : As) + r * ROWB + piece * 16) = pv[t];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < ST; t++) {
+            const int p = tid + 256 * t;
+            if (p < BM * KB) Sx[p % KB][p / KB] = __builtin_bit_cast(float, sv[t]);
+            else if (p < SC) Dw[(p - BM * KB) % KB][(p - BM * KB) / KB] = half_bits_to_float(sv[t]);
+        }
+    };
 
     float acc[TM][TN][16];
 #pragma unroll
@@ -108,32 +162,11 @@ gemm_i8_kernel(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ 
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[a][b][v] = 0.f;
 
+    load_stage(0);
     for (int kb0 = 0; kb0 < nblk; kb0 += KB) {
-        // stage KB blocks of A and B rows (16-byte pieces; out-of-range pieces read 0)
-        for (int p = tid; p < (BM + BN) * KB * 2; p += 256) {
-            const bool isb = p >= BM * KB * 2;
-            const int pp = isb ? p - BM * KB * 2 : p;
-            const int r = pp / (KB * 2), piece = pp % (KB * 2);
-            const int kbyte = kb0 * 32 + piece * 16;
-            const int grow = (isb ? n0 : m0) + r;
-            const bool ok = grow < (isb ? N : M) && kbyte < K;
-            const uint32_t off = ok ? (uint32_t)grow * (uint32_t)K + (uint32_t)kbyte : kOob;
-            const u32x4 v = ld128(isb ? rb : ra, off);
-            *reinterpret_cast<u32x4 *>((isb ? Bs : As) + r * ROWB + piece * 16) = v;
-        }
-        for (int p = tid; p < (BM + BN) * KB; p += 256) {
-            if (p < BM * KB) {
-                const int r = p / KB, kb = p % KB;
-                const int gm = m0 + r, blk = kb0 + kb;
-                Sx[kb][r] = (gm < M && blk < nblk) ? xs[(int64_t)gm * nblk + blk] : 0.f;
-            } else {
-                const int pp = p - BM * KB, c = pp / KB, kb = pp % KB;
-                const int gn = n0 + c, blk = kb0 + kb;
-                const uint16_t h = (gn < N && blk < nblk) ? reinterpret_cast<const uint16_t *>(w.sc)[(int64_t)gn * nblk + blk] : 0;
-                Dw[kb][c] = half_bits_to_float(h);
-            }
-        }
+        store_stage();
         __syncthreads();
+        if (kb0 + KB < nblk) load_stage(kb0 + KB);
         const int kbn = nblk - kb0 < KB ? nblk - kb0 : KB;
         for (int kb = 0; kb < kbn; kb++) {
             i32x4 fa[TM], fb[TN];
@@ -186,12 +219,15 @@ gemm_i8_kernel(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ 
 }
 
 // ---- bf16 variant --------------------------------------------------------------------------
-// grid (ceil(N / BN), ceil(M / BM)), 256 threads. Requires K % 32 == 0.
+// grid (ceil(N / BN), ceil(M / BM)), 256 threads. Requires K % 32 == 0. The next stage's
+// global loads are issued into registers before the current stage is computed.
 template <int BM, int BN, int KB>
 __global__ void __launch_bounds__(256)
 gemm_bf16_kernel(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M) {
     constexpr int ROWB = KB * 64 + 16;  // bf16 row bytes + pad
     constexpr int TM = BM / 64, TN = BN / 64;
+    constexpr int AP = BM * KB * 4, APT = (AP + 255) / 256;  // A: 16-byte pieces (8 bf16)
+    constexpr int BP = BN * KB * 2, BPT = (BP + 255) / 256;  // B: 16-byte pieces (16 int8)
     __shared__ __attribute__((aligned(16))) uint8_t As[BM * ROWB];
     __shared__ __attribute__((aligned(16))) uint8_t Bs[BN * ROWB];
     const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32;
@@ -201,36 +237,44 @@ gemm_bf16_kernel(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, 
     const int wm = wave >> 1, wn = wave & 1;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(x, (uint64_t)M * K * 2);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(w.qs, (uint64_t)N * K);
-    const uint16_t *wsc = reinterpret_cast<const uint16_t *>(w.sc);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(w.sc, (uint64_t)N * nblk * 2);
 
-    f32x16 acc[TM][TN];
+    u32x4 av[APT], bv[BPT];
+    uint32_t dv[BPT];
+    auto load_stage = [&](int kb0) {
 #pragma unroll
-    for (int a = 0; a < TM; a++)
-#pragma unroll
-        for (int b = 0; b < TN; b++) acc[a][b] = f32x16{};
-
-    for (int kb0 = 0; kb0 < nblk; kb0 += KB) {
-        // A: BM rows x KB*64 bytes of bf16 in 16-byte pieces
-        for (int p = tid; p < BM * KB * 4; p += 256) {
+        for (int t = 0; t < APT; t++) {
+            const int p = tid + 256 * t;
             const int r = p / (KB * 4), piece = p % (KB * 4);
-            const int kel = kb0 * 32 + piece * 8;
-            const int gm = m0 + r;
-            const bool ok = gm < M && kel < K;
-            const u32x4 v = ld128(ra, ok ? ((uint32_t)gm * (uint32_t)K + (uint32_t)kel) * 2u : kOob);
-            *reinterpret_cast<u32x4 *>(As + r * ROWB + piece * 16) = v;
+            const int kel = kb0 * 32 + piece * 8, gm = m0 + r;
+            const bool ok = p < AP && gm < M && kel < K;
+            av[t] = ld128(ra, ok ? ((uint32_t)gm * (uint32_t)K + (uint32_t)kel) * 2u : kOob);
         }
-        // B: BN rows x KB*32 int8 in 16-byte pieces, dequantized to bf16(d * q)
-        for (int p = tid; p < BN * KB * 2; p += 256) {
+#pragma unroll
+        for (int t = 0; t < BPT; t++) {
+            const int p = tid + 256 * t;
             const int r = p / (KB * 2), piece = p % (KB * 2);
-            const int blk = kb0 + piece / 2;
-            const int gn = n0 + r;
-            const bool ok = gn < N && blk < nblk;
-            const u32x4 q = ld128(rb, ok ? (uint32_t)gn * (uint32_t)K + (uint32_t)(kb0 * 32 + piece * 16) : kOob);
-            const float d = ok ? half_bits_to_float(wsc[(int64_t)gn * nblk + blk]) : 0.f;
+            const int blk = kb0 + piece / 2, gn = n0 + r;
+            const bool ok = p < BP && gn < N && blk < nblk;
+            bv[t] = ld128(rb, ok ? (uint32_t)gn * (uint32_t)K + (uint32_t)(kb0 * 32 + piece * 16) : kOob);
+            dv[t] = __builtin_amdgcn_raw_buffer_load_b16(rd, ok ? ((uint32_t)gn * nblk + blk) * 2u : kOob, 0, 0);
+        }
+    };
+    auto store_stage = [&]() {
+#pragma unroll
+        for (int t = 0; t < APT; t++) {
+            const int p = tid + 256 * t;
+            if (p < AP) *reinterpret_cast<u32x4 *>(As + (p / (KB * 4)) * ROWB + (p % (KB * 4)) * 16) = av[t];
+        }
+#pragma unroll
+        for (int t = 0; t < BPT; t++) {
+            const int p = tid + 256 * t;
+            if (p >= BP) continue;
+            const float d = half_bits_to_float(dv[t]);
             u32x4 o[2];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t u = q[j];
+                const uint32_t u = bv[t][j];
                 const float f0 = d * (float)(int8_t)(u & 0xFF), f1 = d * (float)(int8_t)((u >> 8) & 0xFF);
                 const float f2 = d * (float)(int8_t)((u >> 16) & 0xFF), f3 = d * (float)(int8_t)(u >> 24);
                 const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f0) |
@@ -240,11 +284,23 @@ gemm_bf16_kernel(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, 
                 o[j >> 1][(j & 1) * 2] = lo;
                 o[j >> 1][(j & 1) * 2 + 1] = hi;
             }
-            uint8_t *dst = Bs + r * ROWB + piece * 32;
+            uint8_t *dst = Bs + (p / (KB * 2)) * ROWB + (p % (KB * 2)) * 32;
             reinterpret_cast<u32x4 *>(dst)[0] = o[0];
             reinterpret_cast<u32x4 *>(dst)[1] = o[1];
         }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; a++)
+#pragma unroll
+        for (int b = 0; b < TN; b++) acc[a][b] = f32x16{};
+
+    load_stage(0);
+    for (int kb0 = 0; kb0 < nblk; kb0 += KB) {
+        store_stage();
         __syncthreads();
+        if (kb0 + KB < nblk) load_stage(kb0 + KB);
         const int ksteps = (nblk - kb0 < KB ? nblk - kb0 : KB) * 2;  // 16-element MFMA steps
         for (int ks = 0; ks < ksteps; ks++) {
             bf16x8 fa[TM], fb[TN];
@@ -287,22 +343,35 @@ hipError_t launch_quantize_act(const uint16_t *x, int64_t m, int64_t k, int8_t *
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs, float *y, int64_t m, hipStream_t s) {
-    if (m <= 0 || w.rows <= 0) return hipSuccess;
-    if (m > 65535 * 128 || w.cols % 32 != 0 || (uint64_t)m * w.cols > 0x7fffffffull) return hipErrorInvalidValue;
-    constexpr int BM = 128, BN = 128, KB = 4;
+template <int BM, int BN, int KB>
+hipError_t launch_i8(const QMat &w, const int8_t *xq, const float *xs, float *y, int64_t m, hipStream_t s) {
     const dim3 grid((unsigned)((w.rows + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
     gemm_i8_kernel<BM, BN, KB><<<grid, 256, 0, s>>>(w, xq, xs, y, (int)m);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s) {
-    if (m <= 0 || w.rows <= 0) return hipSuccess;
-    if (m > 65535 * 128 || w.cols % 32 != 0 || (uint64_t)m * w.cols * 2 > 0x7fffffffull) return hipErrorInvalidValue;
-    constexpr int BM = 128, BN = 128, KB = 2;
+template <int BM, int BN, int KB>
+hipError_t launch_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s) {
     const dim3 grid((unsigned)((w.rows + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
     gemm_bf16_kernel<BM, BN, KB><<<grid, 256, 0, s>>>(w, x, y, (int)m);
     return hipGetLastError();
+}
+
+// Tile shape by M: small M gets small tiles so more workgroups stream W.
+hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs, float *y, int64_t m, hipStream_t s) {
+    if (m <= 0 || w.rows <= 0) return hipSuccess;
+    if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols > 0x7fffffffull) return hipErrorInvalidValue;
+    if (m <= 64) return launch_i8<64, 64, 4>(w, xq, xs, y, m, s);
+    if (m <= 512) return launch_i8<64, 128, 4>(w, xq, xs, y, m, s);
+    return launch_i8<128, 128, 4>(w, xq, xs, y, m, s);
+}
+
+hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s) {
+    if (m <= 0 || w.rows <= 0) return hipSuccess;
+    if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols * 2 > 0x7fffffffull) return hipErrorInvalidValue;
+    if (m <= 64) return launch_bf16<64, 64, 2>(w, x, y, m, s);
+    if (m <= 512) return launch_bf16<64, 128, 2>(w, x, y, m, s);
+    return launch_bf16<128, 128, 2>(w, x, y, m, s);
 }
 
 }  // namespace j4q
