@@ -37,6 +37,9 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5033.0
 BF16_PEAK_TFLOPS = 2517.0
 ROTATE_BYTES = 512 << 20
+# HBM bytes per launch of the headline kernel, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+# counters scaled by a copy kernel of known size (written from those runs; see the .md beside it).
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4_0_n11008_k4096_b1_traffic.json")
 
 
 def log(*a):
@@ -288,6 +291,27 @@ def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n:
     }
 
 
+def calibrate_copy(eng: Engine, nbytes: int = 256 << 20, reps: int = 3) -> None:
+    """Runs the engine's streaming copy kernel on `nbytes` a few times, so a counter profile of
+    this process has a kernel of known traffic to scale the GEMV's byte counters by."""
+    src, dst = eng.hip.malloc(nbytes), eng.hip.malloc(nbytes)
+    for _ in range(reps):
+        check(eng.lib.j4q_copy(C.c_void_p(dst), C.c_void_p(src), nbytes, C.c_void_p(eng.stream)), "copy")
+    eng.hip.sync()
+    eng.hip.free(src)
+    eng.hip.free(dst)
+    log(f"calibration copy: {reps} x {nbytes} bytes")
+
+
+def measured_traffic(workload: str):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return t.get("traffic_bytes_per_launch") if t.get("workload") == workload else None
+
+
 def cpu_baseline(seconds: float = 10.0):
     """The reference's CPU algorithm (CpuQ4Gemm.multiply, restated in C by the oracle) on the
     headline workload, single-threaded on one pinned host core."""
@@ -344,6 +368,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only, no CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="comma list of workload groups to run: gemv,gemm,decode (default all)")
+    ap.add_argument("--calibrate", action="store_true", help="also run a copy kernel of known size (for counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -358,6 +383,8 @@ def main():
         f"sclk={eng.info['max_clock_khz'] / 1e3:.0f} MHz HBM={eng.info['hbm_bytes'] / 2**30:.0f} GiB")
 
     head = gemv_workload(eng, "q4_0_gemv_b1", QuantType.Q4_0, 11008, 4096, 1, args.steps, args.warmup)
+    if args.calibrate:
+        calibrate_copy(eng)
     others = []
     groups = set(filter(None, args.only.split(","))) or {"gemv", "gemm", "decode"}
     if not args.quick:
@@ -406,7 +433,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("q4_0_gemv_b1"),
         },
         "cpu_baseline": cpu,
         "workloads": [head] + others,

@@ -180,6 +180,9 @@ int j4q_synth_bf16_device(uint64_t seed, int64_t n, uint16_t *device_out, void *
 /* Occupies `stream` for `microseconds` (<= 10 s) of device wall-clock time, so a host can
  * queue many short launches behind it and time them back to back with events. */
 int j4q_spin(uint32_t microseconds, void *stream);
+/* Streaming copy of `nbytes` (a multiple of 16; both pointers 16-byte aligned) with 128-bit
+ * loads and stores: a kernel of known traffic, used to scale HBM byte counters. */
+int j4q_copy(void *device_dst, const void *device_src, uint64_t nbytes, void *stream);
 
 #ifdef __cplusplus
 }

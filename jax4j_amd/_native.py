@@ -93,6 +93,7 @@ SIGNATURES = {
     "j4q_synth_f32_device": [_u64, _i64, _vp, _vp],
     "j4q_synth_bf16_device": [_u64, _i64, _vp, _vp],
     "j4q_spin": [C.c_uint32, _vp],
+    "j4q_copy": [_vp, _vp, _u64, _vp],
 }
 _RESTYPES = {"j4q_last_error": C.c_char_p}
 

@@ -680,4 +680,15 @@ int j4q_spin(uint32_t microseconds, void *stream) {
     return J4Q_OK;
 }
 
+int j4q_copy(void *dst, const void *src, uint64_t nbytes, void *stream) {
+    if (!dst || !src) return fail(J4Q_EINVAL, "copy: NULL pointer");
+    if (nbytes % 16 != 0 || !aligned(dst, 16) || !aligned(src, 16))
+        return fail(J4Q_EINVAL, "copy: nbytes must be a multiple of 16 and both pointers 16-byte aligned");
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = ensure_ready();
+    if (rc) return rc;
+    HIP_TRY("copy", j4q::launch_copy(dst, src, nbytes, pick_stream(stream)));
+    return J4Q_OK;
+}
+
 }  // extern "C"

@@ -380,6 +380,21 @@ __global__ void spin_kernel(uint64_t ticks) {
 }
 }  // namespace
 
+typedef uint32_t cu32x4 __attribute__((ext_vector_type(4)));
+
+// Grid-stride 128-bit copy: reads and writes each byte exactly once.
+__global__ void __launch_bounds__(256) copy_kernel(const cu32x4 *__restrict__ src, cu32x4 *__restrict__ dst, uint64_t n16) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_copy(void *dst, const void *src, uint64_t nbytes, hipStream_t s) {
+    const uint64_t n16 = nbytes / 16;
+    if (n16 == 0) return hipSuccess;
+    const uint64_t want = (n16 + 255) / 256;
+    copy_kernel<<<(unsigned)(want < 4096 ? want : 4096), 256, 0, s>>>((const cu32x4 *)src, (cu32x4 *)dst, n16);
+    return hipGetLastError();
+}
+
 hipError_t launch_spin(uint32_t microseconds, int wall_clock_khz, hipStream_t s) {
     const uint64_t ticks = (uint64_t)microseconds * (uint64_t)(wall_clock_khz > 0 ? wall_clock_khz : 100000) / 1000u;
     spin_kernel<<<1, 64, 0, s>>>(ticks);
