@@ -35,9 +35,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint6
     const uint32_t n = bytes > 0x7fffffffull ? 0x7fffffffu : (uint32_t)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)n, 0x00020000);
 }
-__device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 
 // One thread per (row, 32-element block): s = amax/127, q = clamp(roundf(x * (1/s)), +-127)
 // (ggml quantize_row_q8_0 with the scale kept in fp32). Division and the reciprocal are
@@ -81,76 +78,157 @@ quantize_act_kernel(const uint16_t *__restrict__ x, int64_t m, int64_t k, int8_t
 // Row index of result element v of `lane` inside a 32 x 32 MFMA tile.
 __device__ __forceinline__ int mfma_row(int lane, int v) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
-// ---- int8 variant --------------------------------------------------------------------------
-// grid (ceil(N / BN), ceil(M / BM)), 256 threads. Requires K % 32 == 0. The next stage's
-// global loads are issued into registers before the current stage is computed.
-template <int BM, int BN, int KB>
+// ---- the GEMM kernel (both variants) ------------------------------------------------------
+// A workgroup of 4 waves (2 x 2) computes a BM x BN tile of Y over all of K in stages of KB
+// Q8_0 blocks. Global loads run R stages ahead in a ring of R register sets (each set only
+// ever written by its own loads, so no in-flight register is copied); a stage is written to
+// one of two LDS buffers (the bf16 variant dequantizes W on the way), then one barrier, then
+// the next loads are issued and the stage is computed. With two LDS buffers a single barrier
+// per stage suffices: a buffer is rewritten only after every wave has passed the barrier
+// that follows its last use.
+enum { kVarInt8 = 0, kVarBf16 = 1 };
+
+template <int VAR, int BM, int BN, int KB, int R>
 __global__ void __launch_bounds__(256)
-gemm_i8_kernel(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs, float *__restrict__ y, int M) {
-    constexpr int ROWB = KB * 32 + 16;
-    constexpr int TM = BM / 64, TN = BN / 64;  // 32 x 32 tiles per wave
-    constexpr int PIECES = (BM + BN) * KB * 2;  // 16-byte pieces per stage
-    constexpr int PT = (PIECES + 255) / 256;
-    constexpr int SC = (BM + BN) * KB;  // scales per stage
-    constexpr int ST = (SC + 255) / 256;
-    __shared__ __attribute__((aligned(16))) int8_t As[BM * ROWB];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[BN * ROWB];
-    __shared__ __attribute__((aligned(16))) float Sx[KB][BM];
-    __shared__ float Dw[KB][BN];
+gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, float *__restrict__ y, int M) {
+    constexpr int EB = VAR == kVarInt8 ? 1 : 2;     // bytes per activation element
+    constexpr int AROW = KB * 32 * EB;              // A bytes per row per stage
+    constexpr int BROW = KB * 32 * EB;              // B bytes per row per stage in LDS (bf16: dequantized)
+    constexpr int ALD = AROW + 16, BLD = BROW + 16; // padded LDS row strides
+    constexpr int TM = BM / 64, TN = BN / 64;       // 32 x 32 tiles per wave
+    constexpr int AP = BM * AROW / 16, APT = (AP + 255) / 256;  // A 16-byte pieces per stage
+    constexpr int BP = BN * KB * 2, BPT = (BP + 255) / 256;     // B 16-byte int8 pieces per stage
+    constexpr int XP = VAR == kVarInt8 ? BM * KB : 0, XPT = (XP + 255) / 256;  // activation scales
+    // W scales: the int8 variant stages them in LDS (one slot per thread, no branch); the bf16
+    // variant needs one per B piece for the dequantization.
+    constexpr int DP = VAR == kVarInt8 ? BN * KB : BP, DPT = (DP + 255) / 256;
+    constexpr int ABUF = BM * ALD, BBUF = BN * BLD;
+    __shared__ __attribute__((aligned(16))) uint8_t As[2][ABUF];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BBUF];
+    __shared__ __attribute__((aligned(16))) float Sx[2][KB][VAR == kVarInt8 ? BM : 4];
+    __shared__ float Dw[2][KB][VAR == kVarInt8 ? BN : 4];
+
     const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32;
-    const int n0 = (int)blockIdx.x * BN, m0 = (int)blockIdx.y * BM;
+    const int nst = (nblk + KB - 1) / KB;
+    // XCD-aware tile order: workgroup b runs on XCD b % 8, so when the tile count divides by 8
+    // each XCD takes a contiguous range of tiles, M-fastest: the tiles one XCD runs at a time
+    // share their W rows (and X) in that XCD's L2.
+    const int mt = (M + BM - 1) / BM, tiles = (int)gridDim.x;
+    int t = (int)blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    const int n0 = (t / mt) * BN, m0 = (t % mt) * BM;
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(xq, (uint64_t)M * K);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(xv, (uint64_t)M * K * EB);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(w.qs, (uint64_t)N * K);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(xs, (uint64_t)M * nblk * 4);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(w.sc, (uint64_t)N * nblk * 2);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(xs, VAR == kVarInt8 ? (uint64_t)M * nblk * 4 : 0);
 
-    u32x4 pv[PT];
-    uint32_t sv[ST];
-    auto load_stage = [&](int kb0) {
+    struct Set {
+        u32x4 a[APT], b[BPT];
+        uint32_t d[DPT], x[XPT > 0 ? XPT : 1];
+    };
+    Set set[R];
+
+    // Per-thread byte offsets of stage 0 (a stage advances every section by a wave-uniform
+    // amount, passed as the buffer instruction's scalar offset). Pieces outside the matrix
+    // get an out-of-range offset; pieces past K in the last stage read real bytes that the
+    // compute never uses (it stops at the last block).
+    uint32_t aoff[APT], boff[BPT], doff[DPT], xoff[XPT > 0 ? XPT : 1];
 #pragma unroll
-        for (int t = 0; t < PT; t++) {
-            const int p = tid + 256 * t;
-            const bool isb = p >= BM * KB * 2;
-            const int pp = isb ? p - BM * KB * 2 : p;
-            const int r = pp / (KB * 2), piece = pp % (KB * 2);
-            const int kbyte = kb0 * 32 + piece * 16;
-            const int grow = (isb ? n0 : m0) + r;
-            const bool ok = p < PIECES && grow < (isb ? N : M) && kbyte < K;
-            pv[t] = ld128(isb ? rb : ra, ok ? (uint32_t)grow * (uint32_t)K + (uint32_t)kbyte : kOob);
+    for (int t = 0; t < APT; t++) {
+        const int p = tid + 256 * t;
+        const int r = p / (AROW / 16), piece = p % (AROW / 16), gm = m0 + r;
+        aoff[t] = (p < AP && gm < M) ? (uint32_t)gm * (uint32_t)K * EB + (uint32_t)piece * 16u : kOob;
+    }
+#pragma unroll
+    for (int t = 0; t < BPT; t++) {
+        const int p = tid + 256 * t;
+        const int r = p / (KB * 2), piece = p % (KB * 2), gn = n0 + r;
+        const bool ok = p < BP && gn < N;
+        boff[t] = ok ? (uint32_t)gn * (uint32_t)K + (uint32_t)piece * 16u : kOob;
+        if constexpr (VAR == kVarBf16) doff[t] = ok ? ((uint32_t)gn * nblk + (uint32_t)(piece / 2)) * 2u : kOob;
+    }
+    if constexpr (VAR == kVarInt8) {
+#pragma unroll
+        for (int t = 0; t < DPT; t++) {
+            const int p = tid + 256 * t, gn = n0 + p / KB;
+            doff[t] = (p < DP && gn < N) ? ((uint32_t)gn * nblk + (uint32_t)(p % KB)) * 2u : kOob;
         }
+    }
+    if constexpr (VAR == kVarInt8) {
 #pragma unroll
-        for (int t = 0; t < ST; t++) {
-            const int p = tid + 256 * t;
-            if (p < BM * KB) {
-                const int gm = m0 + p / KB, blk = kb0 + p % KB;
-                const bool ok = gm < M && blk < nblk;
-                sv[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? ((uint32_t)gm * nblk + blk) * 4u : kOob, 0, 0);
-            } else {
-                const int pp = p - BM * KB, gn = n0 + pp / KB, blk = kb0 + pp % KB;
-                const bool ok = p < SC && gn < N && blk < nblk;
-                sv[t] = __builtin_amdgcn_raw_buffer_load_b16(rd, ok ? ((uint32_t)gn * nblk + blk) * 2u : kOob, 0, 0);
-            }
+        for (int t = 0; t < XPT; t++) {
+            const int p = tid + 256 * t, gm = m0 + p / KB;
+            xoff[t] = (p < XP && gm < M) ? ((uint32_t)gm * nblk + (uint32_t)(p % KB)) * 4u : kOob;
+        }
+    }
+
+    // Stage st's loads; stages past the end read an out-of-range offset (zeros, no traffic).
+    auto load = [&](int st, Set &S) {
+        const bool live = st < nst;
+        const uint32_t kb0 = (uint32_t)(st * KB);
+        const uint32_t sa = live ? kb0 * 32u * EB : kOob, sb = live ? kb0 * 32u : kOob;
+        const uint32_t sd = live ? kb0 * 2u : kOob, sx = live ? kb0 * 4u : kOob;
+#pragma unroll
+        for (int t = 0; t < APT; t++)
+            S.a[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[t], sa, 0));
+#pragma unroll
+        for (int t = 0; t < BPT; t++)
+            S.b[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[t], sb, 0));
+#pragma unroll
+        for (int t = 0; t < DPT; t++) S.d[t] = __builtin_amdgcn_raw_buffer_load_b16(rd, doff[t], sd, 0);
+        if constexpr (VAR == kVarInt8) {
+#pragma unroll
+            for (int t = 0; t < XPT; t++) S.x[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, xoff[t], sx, 0);
         }
     };
-    auto store_stage = [&]() {
+
+    // Writes a stage into LDS buffer `bi`.
+    auto store = [&](const Set &S, int bi) {
 #pragma unroll
-        for (int t = 0; t < PT; t++) {
+        for (int t = 0; t < APT; t++) {
             const int p = tid + 256 * t;
-            if (p < PIECES) {
-                const bool isb = p >= BM * KB * 2;
-                const int pp = isb ? p - BM * KB * 2 : p;
-                const int r = pp / (KB * 2), piece = pp % (KB * 2);
-                *reinterpret_cast<u32x4 *>((isb ? Bs : As) + r * ROWB + piece * 16) = pv[t];
-            }
+            if (APT * 256 == AP || p < AP) *reinterpret_cast<u32x4 *>(&As[bi][(p / (AROW / 16)) * ALD + (p % (AROW / 16)) * 16]) = S.a[t];
         }
 #pragma unroll
-        for (int t = 0; t < ST; t++) {
+        for (int t = 0; t < BPT; t++) {
             const int p = tid + 256 * t;
-            if (p < BM * KB) Sx[p % KB][p / KB] = __builtin_bit_cast(float, sv[t]);
-            else if (p < SC) Dw[(p - BM * KB) % KB][(p - BM * KB) / KB] = half_bits_to_float(sv[t]);
+            if (BPT * 256 != BP && p >= BP) continue;
+            const int r = p / (KB * 2), piece = p % (KB * 2);
+            if constexpr (VAR == kVarInt8) {
+                *reinterpret_cast<u32x4 *>(&Bs[bi][r * BLD + piece * 16]) = S.b[t];
+            } else {
+                // bf16(d * q): d * q is exact in fp32, the conversion rounds to nearest even
+                const float d = half_bits_to_float(S.d[t]);
+                u32x4 o[2];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t u = S.b[t][j];
+                    const float f0 = d * (float)(int8_t)(u & 0xFF), f1 = d * (float)(int8_t)((u >> 8) & 0xFF);
+                    const float f2 = d * (float)(int8_t)((u >> 16) & 0xFF), f3 = d * (float)(int8_t)(u >> 24);
+                    o[j >> 1][(j & 1) * 2] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f0) |
+                                             ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f1) << 16);
+                    o[j >> 1][(j & 1) * 2 + 1] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f2) |
+                                                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f3) << 16);
+                }
+                uint8_t *dst = &Bs[bi][r * BLD + piece * 32];
+                reinterpret_cast<u32x4 *>(dst)[0] = o[0];
+                reinterpret_cast<u32x4 *>(dst)[1] = o[1];
+            }
+        }
+        if constexpr (VAR == kVarInt8) {
+#pragma unroll
+            for (int t = 0; t < XPT; t++) {
+                const int p = tid + 256 * t;
+                if (XPT * 256 == XP || p < XP) Sx[bi][p % KB][p / KB] = __builtin_bit_cast(float, S.x[t]);
+            }
+#pragma unroll
+            for (int t = 0; t < DPT; t++) {
+                const int p = tid + 256 * t;
+                if (DPT * 256 == DP || p < DP) Dw[bi][p % KB][p / KB] = half_bits_to_float(S.d[t]);
+            }
         }
     };
 
@@ -162,165 +240,96 @@ gemm_i8_kernel(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ 
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[a][b][v] = 0.f;
 
-    load_stage(0);
-    for (int kb0 = 0; kb0 < nblk; kb0 += KB) {
-        store_stage();
-        __syncthreads();
-        if (kb0 + KB < nblk) load_stage(kb0 + KB);
-        const int kbn = nblk - kb0 < KB ? nblk - kb0 : KB;
-        for (int kb = 0; kb < kbn; kb++) {
-            i32x4 fa[TM], fb[TN];
-            float dw[TN];
+    // Computes stage st from LDS buffer bi.
+    auto compute = [&](int st, int bi) {
+        const int kbn = nblk - st * KB < KB ? nblk - st * KB : KB;
+        if constexpr (VAR == kVarInt8) {
+            for (int kb = 0; kb < kbn; kb++) {
+                i32x4 fa[TM], fb[TN];
+                float dw[TN];
 #pragma unroll
-            for (int a = 0; a < TM; a++) {
-                const int r = wm * (BM / 2) + a * 32 + (lane & 31);
-                fa[a] = *reinterpret_cast<const i32x4 *>(As + r * ROWB + kb * 32 + (lane >> 5) * 16);
-            }
-#pragma unroll
-            for (int b = 0; b < TN; b++) {
-                const int c = wn * (BN / 2) + b * 32 + (lane & 31);
-                fb[b] = *reinterpret_cast<const i32x4 *>(Bs + c * ROWB + kb * 32 + (lane >> 5) * 16);
-                dw[b] = Dw[kb][c];
-            }
-#pragma unroll
-            for (int a = 0; a < TM; a++) {
-                float sx[16];
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const f32x4 t = *reinterpret_cast<const f32x4 *>(&Sx[kb][wm * (BM / 2) + a * 32 + 8 * g + 4 * (lane >> 5)]);
-                    sx[4 * g] = t.x;
-                    sx[4 * g + 1] = t.y;
-                    sx[4 * g + 2] = t.z;
-                    sx[4 * g + 3] = t.w;
+                for (int a = 0; a < TM; a++) {
+                    const int r = wm * (BM / 2) + a * 32 + (lane & 31);
+                    fa[a] = *reinterpret_cast<const i32x4 *>(&As[bi][r * ALD + kb * 32 + (lane >> 5) * 16]);
                 }
 #pragma unroll
                 for (int b = 0; b < TN; b++) {
-                    const i32x16 zero = {};
-                    const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], zero, 0, 0, 0);
+                    const int c = wn * (BN / 2) + b * 32 + (lane & 31);
+                    fb[b] = *reinterpret_cast<const i32x4 *>(&Bs[bi][c * BLD + kb * 32 + (lane >> 5) * 16]);
+                    dw[b] = Dw[bi][kb][c];
+                }
 #pragma unroll
-                    for (int v = 0; v < 16; v++)
-                        acc[a][b][v] = __builtin_fmaf((float)I[v], __fmul_rn(sx[v], dw[b]), acc[a][b][v]);
+                for (int a = 0; a < TM; a++) {
+                    float sx[16];
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const f32x4 t = *reinterpret_cast<const f32x4 *>(&Sx[bi][kb][wm * (BM / 2) + a * 32 + 8 * g + 4 * (lane >> 5)]);
+                        sx[4 * g] = t.x;
+                        sx[4 * g + 1] = t.y;
+                        sx[4 * g + 2] = t.z;
+                        sx[4 * g + 3] = t.w;
+                    }
+#pragma unroll
+                    for (int b = 0; b < TN; b++) {
+                        const i32x16 zero = {};
+                        const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], zero, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 16; v++)
+                            acc[a][b][v] = __builtin_fmaf((float)I[v], __fmul_rn(sx[v], dw[b]), acc[a][b][v]);
+                    }
                 }
             }
-        }
-        __syncthreads();
-    }
+        } else {
+            for (int ks = 0; ks < kbn * 2; ks++) {  // 16-element MFMA steps
+                bf16x8 fa[TM], fb[TN];
 #pragma unroll
-    for (int a = 0; a < TM; a++)
+                for (int a = 0; a < TM; a++) {
+                    const int r = wm * (BM / 2) + a * 32 + (lane & 31);
+                    fa[a] = *reinterpret_cast<const bf16x8 *>(&As[bi][r * ALD + ks * 32 + (lane >> 5) * 16]);
+                }
 #pragma unroll
-        for (int b = 0; b < TN; b++) {
-            const int col = n0 + wn * (BN / 2) + b * 32 + (lane & 31);
+                for (int b = 0; b < TN; b++) {
+                    const int c = wn * (BN / 2) + b * 32 + (lane & 31);
+                    fb[b] = *reinterpret_cast<const bf16x8 *>(&Bs[bi][c * BLD + ks * 32 + (lane >> 5) * 16]);
+                }
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int row = m0 + wm * (BM / 2) + a * 32 + mfma_row(lane, v);
-                if (row < M && col < N) y[(int64_t)row * N + col] = acc[a][b][v];
+                for (int a = 0; a < TM; a++)
+#pragma unroll
+                    for (int b = 0; b < TN; b++) {
+                        f32x16 c;
+#pragma unroll
+                        for (int v = 0; v < 16; v++) c[v] = acc[a][b][v];
+                        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], c, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 16; v++) acc[a][b][v] = c[v];
+                    }
             }
-        }
-}
-
-// ---- bf16 variant --------------------------------------------------------------------------
-// grid (ceil(N / BN), ceil(M / BM)), 256 threads. Requires K % 32 == 0. The next stage's
-// global loads are issued into registers before the current stage is computed.
-template <int BM, int BN, int KB>
-__global__ void __launch_bounds__(256)
-gemm_bf16_kernel(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M) {
-    constexpr int ROWB = KB * 64 + 16;  // bf16 row bytes + pad
-    constexpr int TM = BM / 64, TN = BN / 64;
-    constexpr int AP = BM * KB * 4, APT = (AP + 255) / 256;  // A: 16-byte pieces (8 bf16)
-    constexpr int BP = BN * KB * 2, BPT = (BP + 255) / 256;  // B: 16-byte pieces (16 int8)
-    __shared__ __attribute__((aligned(16))) uint8_t As[BM * ROWB];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[BN * ROWB];
-    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32;
-    const int n0 = (int)blockIdx.x * BN, m0 = (int)blockIdx.y * BM;
-    const int tid = (int)threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(x, (uint64_t)M * K * 2);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(w.qs, (uint64_t)N * K);
-    const __amdgpu_buffer_rsrc_t rd = make_rsrc(w.sc, (uint64_t)N * nblk * 2);
-
-    u32x4 av[APT], bv[BPT];
-    uint32_t dv[BPT];
-    auto load_stage = [&](int kb0) {
-#pragma unroll
-        for (int t = 0; t < APT; t++) {
-            const int p = tid + 256 * t;
-            const int r = p / (KB * 4), piece = p % (KB * 4);
-            const int kel = kb0 * 32 + piece * 8, gm = m0 + r;
-            const bool ok = p < AP && gm < M && kel < K;
-            av[t] = ld128(ra, ok ? ((uint32_t)gm * (uint32_t)K + (uint32_t)kel) * 2u : kOob);
-        }
-#pragma unroll
-        for (int t = 0; t < BPT; t++) {
-            const int p = tid + 256 * t;
-            const int r = p / (KB * 2), piece = p % (KB * 2);
-            const int blk = kb0 + piece / 2, gn = n0 + r;
-            const bool ok = p < BP && gn < N && blk < nblk;
-            bv[t] = ld128(rb, ok ? (uint32_t)gn * (uint32_t)K + (uint32_t)(kb0 * 32 + piece * 16) : kOob);
-            dv[t] = __builtin_amdgcn_raw_buffer_load_b16(rd, ok ? ((uint32_t)gn * nblk + blk) * 2u : kOob, 0, 0);
-        }
-    };
-    auto store_stage = [&]() {
-#pragma unroll
-        for (int t = 0; t < APT; t++) {
-            const int p = tid + 256 * t;
-            if (p < AP) *reinterpret_cast<u32x4 *>(As + (p / (KB * 4)) * ROWB + (p % (KB * 4)) * 16) = av[t];
-        }
-#pragma unroll
-        for (int t = 0; t < BPT; t++) {
-            const int p = tid + 256 * t;
-            if (p >= BP) continue;
-            const float d = half_bits_to_float(dv[t]);
-            u32x4 o[2];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t u = bv[t][j];
-                const float f0 = d * (float)(int8_t)(u & 0xFF), f1 = d * (float)(int8_t)((u >> 8) & 0xFF);
-                const float f2 = d * (float)(int8_t)((u >> 16) & 0xFF), f3 = d * (float)(int8_t)(u >> 24);
-                const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f0) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f1) << 16);
-                const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f2) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f3) << 16);
-                o[j >> 1][(j & 1) * 2] = lo;
-                o[j >> 1][(j & 1) * 2 + 1] = hi;
-            }
-            uint8_t *dst = Bs + (p / (KB * 2)) * ROWB + (p % (KB * 2)) * 32;
-            reinterpret_cast<u32x4 *>(dst)[0] = o[0];
-            reinterpret_cast<u32x4 *>(dst)[1] = o[1];
         }
     };
 
-    f32x16 acc[TM][TN];
+    // Issue the prologue sets in ring order (the scheduler may not interleave them): the wait
+    // before each store then counts exactly the younger sets' loads.
 #pragma unroll
-    for (int a = 0; a < TM; a++)
-#pragma unroll
-        for (int b = 0; b < TN; b++) acc[a][b] = f32x16{};
-
-    load_stage(0);
-    for (int kb0 = 0; kb0 < nblk; kb0 += KB) {
-        store_stage();
-        __syncthreads();
-        if (kb0 + KB < nblk) load_stage(kb0 + KB);
-        const int ksteps = (nblk - kb0 < KB ? nblk - kb0 : KB) * 2;  // 16-element MFMA steps
-        for (int ks = 0; ks < ksteps; ks++) {
-            bf16x8 fa[TM], fb[TN];
-#pragma unroll
-            for (int a = 0; a < TM; a++) {
-                const int r = wm * (BM / 2) + a * 32 + (lane & 31);
-                fa[a] = *reinterpret_cast<const bf16x8 *>(As + r * ROWB + ks * 32 + (lane >> 5) * 16);
-            }
-#pragma unroll
-            for (int b = 0; b < TN; b++) {
-                const int c = wn * (BN / 2) + b * 32 + (lane & 31);
-                fb[b] = *reinterpret_cast<const bf16x8 *>(Bs + c * ROWB + ks * 32 + (lane >> 5) * 16);
-            }
-#pragma unroll
-            for (int a = 0; a < TM; a++)
-#pragma unroll
-                for (int b = 0; b < TN; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
-        }
-        __syncthreads();
+    for (int r = 0; r < R; r++) {
+        load(r, set[r]);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    // No early exit inside the ring: a stage past the end loads nothing (out-of-range
+    // offsets), stores zeros and computes no blocks. An exit here would make the wait
+    // before each store conservative (vmcnt(0)) and drain the ring every R stages.
+    for (int base = 0; base < nst; base += R) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int st = base + r;
+            const int bi = st & 1;
+            store(set[r], bi);
+            __syncthreads();
+            load(st + R, set[r]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(st, bi);
+        }
+    }
+
 #pragma unroll
     for (int a = 0; a < TM; a++)
 #pragma unroll
@@ -343,17 +352,11 @@ hipError_t launch_quantize_act(const uint16_t *x, int64_t m, int64_t k, int8_t *
     return hipGetLastError();
 }
 
-template <int BM, int BN, int KB>
-hipError_t launch_i8(const QMat &w, const int8_t *xq, const float *xs, float *y, int64_t m, hipStream_t s) {
-    const dim3 grid((unsigned)((w.rows + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
-    gemm_i8_kernel<BM, BN, KB><<<grid, 256, 0, s>>>(w, xq, xs, y, (int)m);
-    return hipGetLastError();
-}
-
-template <int BM, int BN, int KB>
-hipError_t launch_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s) {
-    const dim3 grid((unsigned)((w.rows + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
-    gemm_bf16_kernel<BM, BN, KB><<<grid, 256, 0, s>>>(w, x, y, (int)m);
+template <int VAR, int BM, int BN, int KB, int R>
+hipError_t launch_gemm(const QMat &w, const void *x, const float *xs, float *y, int64_t m, hipStream_t s) {
+    const uint64_t tiles = (uint64_t)((w.rows + BN - 1) / BN) * (uint64_t)((m + BM - 1) / BM);
+    if (tiles > 0x7fffffffu) return hipErrorInvalidValue;
+    gemm_kernel<VAR, BM, BN, KB, R><<<(unsigned)tiles, 256, 0, s>>>(w, x, xs, y, (int)m);
     return hipGetLastError();
 }
 
@@ -361,17 +364,17 @@ hipError_t launch_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hi
 hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs, float *y, int64_t m, hipStream_t s) {
     if (m <= 0 || w.rows <= 0) return hipSuccess;
     if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols > 0x7fffffffull) return hipErrorInvalidValue;
-    if (m <= 64) return launch_i8<64, 64, 4>(w, xq, xs, y, m, s);
-    if (m <= 512) return launch_i8<64, 128, 4>(w, xq, xs, y, m, s);
-    return launch_i8<128, 128, 4>(w, xq, xs, y, m, s);
+    if (m <= 64) return launch_gemm<kVarInt8, 64, 64, 8, 3>(w, xq, xs, y, m, s);
+    if (m <= 512) return launch_gemm<kVarInt8, 64, 128, 4, 4>(w, xq, xs, y, m, s);
+    return launch_gemm<kVarInt8, 128, 128, 4, 3>(w, xq, xs, y, m, s);
 }
 
 hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s) {
     if (m <= 0 || w.rows <= 0) return hipSuccess;
     if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols * 2 > 0x7fffffffull) return hipErrorInvalidValue;
-    if (m <= 64) return launch_bf16<64, 64, 2>(w, x, y, m, s);
-    if (m <= 512) return launch_bf16<64, 128, 2>(w, x, y, m, s);
-    return launch_bf16<128, 128, 2>(w, x, y, m, s);
+    if (m <= 64) return launch_gemm<kVarBf16, 64, 64, 4, 3>(w, x, nullptr, y, m, s);
+    if (m <= 512) return launch_gemm<kVarBf16, 128, 64, 2, 4>(w, x, nullptr, y, m, s);
+    return launch_gemm<kVarBf16, 128, 128, 2, 3>(w, x, nullptr, y, m, s);
 }
 
 }  // namespace j4q
