@@ -88,20 +88,21 @@ __device__ __forceinline__ int mfma_row(int lane, int v) { return 8 * (v >> 2) +
 // that follows its last use.
 enum { kVarInt8 = 0, kVarBf16 = 1 };
 
-template <int VAR, int BM, int BN, int KB, int R>
-__global__ void __launch_bounds__(256)
+template <int VAR, int BM, int BN, int KB, int R, int G>
+__global__ void __launch_bounds__(256 * G)
 gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, float *__restrict__ y, int M) {
+    constexpr int T = 256 * G;                      // threads
     constexpr int EB = VAR == kVarInt8 ? 1 : 2;     // bytes per activation element
     constexpr int AROW = KB * 32 * EB;              // A bytes per row per stage
     constexpr int BROW = KB * 32 * EB;              // B bytes per row per stage in LDS (bf16: dequantized)
     constexpr int ALD = AROW + 16, BLD = BROW + 16; // padded LDS row strides
     constexpr int TM = BM / 64, TN = BN / 64;       // 32 x 32 tiles per wave
-    constexpr int AP = BM * AROW / 16, APT = (AP + 255) / 256;  // A 16-byte pieces per stage
-    constexpr int BP = BN * KB * 2, BPT = (BP + 255) / 256;     // B 16-byte int8 pieces per stage
-    constexpr int XP = VAR == kVarInt8 ? BM * KB : 0, XPT = (XP + 255) / 256;  // activation scales
+    constexpr int AP = BM * AROW / 16, APT = (AP + T - 1) / T;  // A 16-byte pieces per stage
+    constexpr int BP = BN * KB * 2, BPT = (BP + T - 1) / T;     // B 16-byte int8 pieces per stage
+    constexpr int XP = VAR == kVarInt8 ? BM * KB : 0, XPT = (XP + T - 1) / T;  // activation scales
     // W scales: the int8 variant stages them in LDS (one slot per thread, no branch); the bf16
     // variant needs one per B piece for the dequantization.
-    constexpr int DP = VAR == kVarInt8 ? BN * KB : BP, DPT = (DP + 255) / 256;
+    constexpr int DP = VAR == kVarInt8 ? BN * KB : BP, DPT = (DP + T - 1) / T;
     constexpr int ABUF = BM * ALD, BBUF = BN * BLD;
     __shared__ __attribute__((aligned(16))) uint8_t As[2][ABUF];
     __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BBUF];
@@ -119,7 +120,9 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
     const int n0 = (t / mt) * BN, m0 = (t % mt) * BM;
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    // waves 4g .. 4g+3 form group g (2 x 2 over the tile); group g computes its share of every
+    // stage's k range, and the groups' partial tiles are added at the end
+    const int grp = wave >> 2, wm = (wave & 3) >> 1, wn = wave & 1;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(xv, (uint64_t)M * K * EB);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(w.qs, (uint64_t)N * K);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(w.sc, (uint64_t)N * nblk * 2);
@@ -138,13 +141,13 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
     uint32_t aoff[APT], boff[BPT], doff[DPT], xoff[XPT > 0 ? XPT : 1];
 #pragma unroll
     for (int t = 0; t < APT; t++) {
-        const int p = tid + 256 * t;
+        const int p = tid + T * t;
         const int r = p / (AROW / 16), piece = p % (AROW / 16), gm = m0 + r;
         aoff[t] = (p < AP && gm < M) ? (uint32_t)gm * (uint32_t)K * EB + (uint32_t)piece * 16u : kOob;
     }
 #pragma unroll
     for (int t = 0; t < BPT; t++) {
-        const int p = tid + 256 * t;
+        const int p = tid + T * t;
         const int r = p / (KB * 2), piece = p % (KB * 2), gn = n0 + r;
         const bool ok = p < BP && gn < N;
         boff[t] = ok ? (uint32_t)gn * (uint32_t)K + (uint32_t)piece * 16u : kOob;
@@ -153,14 +156,14 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
     if constexpr (VAR == kVarInt8) {
 #pragma unroll
         for (int t = 0; t < DPT; t++) {
-            const int p = tid + 256 * t, gn = n0 + p / KB;
+            const int p = tid + T * t, gn = n0 + p / KB;
             doff[t] = (p < DP && gn < N) ? ((uint32_t)gn * nblk + (uint32_t)(p % KB)) * 2u : kOob;
         }
     }
     if constexpr (VAR == kVarInt8) {
 #pragma unroll
         for (int t = 0; t < XPT; t++) {
-            const int p = tid + 256 * t, gm = m0 + p / KB;
+            const int p = tid + T * t, gm = m0 + p / KB;
             xoff[t] = (p < XP && gm < M) ? ((uint32_t)gm * nblk + (uint32_t)(p % KB)) * 4u : kOob;
         }
     }
@@ -189,13 +192,13 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
     auto store = [&](const Set &S, int bi) {
 #pragma unroll
         for (int t = 0; t < APT; t++) {
-            const int p = tid + 256 * t;
-            if (APT * 256 == AP || p < AP) *reinterpret_cast<u32x4 *>(&As[bi][(p / (AROW / 16)) * ALD + (p % (AROW / 16)) * 16]) = S.a[t];
+            const int p = tid + T * t;
+            if (APT * T == AP || p < AP) *reinterpret_cast<u32x4 *>(&As[bi][(p / (AROW / 16)) * ALD + (p % (AROW / 16)) * 16]) = S.a[t];
         }
 #pragma unroll
         for (int t = 0; t < BPT; t++) {
-            const int p = tid + 256 * t;
-            if (BPT * 256 != BP && p >= BP) continue;
+            const int p = tid + T * t;
+            if (BPT * T != BP && p >= BP) continue;
             const int r = p / (KB * 2), piece = p % (KB * 2);
             if constexpr (VAR == kVarInt8) {
                 *reinterpret_cast<u32x4 *>(&Bs[bi][r * BLD + piece * 16]) = S.b[t];
@@ -221,13 +224,13 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
         if constexpr (VAR == kVarInt8) {
 #pragma unroll
             for (int t = 0; t < XPT; t++) {
-                const int p = tid + 256 * t;
-                if (XPT * 256 == XP || p < XP) Sx[bi][p % KB][p / KB] = __builtin_bit_cast(float, S.x[t]);
+                const int p = tid + T * t;
+                if (XPT * T == XP || p < XP) Sx[bi][p % KB][p / KB] = __builtin_bit_cast(float, S.x[t]);
             }
 #pragma unroll
             for (int t = 0; t < DPT; t++) {
-                const int p = tid + 256 * t;
-                if (DPT * 256 == DP || p < DP) Dw[bi][p % KB][p / KB] = half_bits_to_float(S.d[t]);
+                const int p = tid + T * t;
+                if (DPT * T == DP || p < DP) Dw[bi][p % KB][p / KB] = half_bits_to_float(S.d[t]);
             }
         }
     };
@@ -240,72 +243,68 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[a][b][v] = 0.f;
 
-    // Computes stage st from LDS buffer bi.
-    auto compute = [&](int st, int bi) {
-        const int kbn = nblk - st * KB < KB ? nblk - st * KB : KB;
+    // One Q8_0 block (int8) or one 16-element step (bf16) of a stage held in LDS buffer bi.
+    auto step = [&](int bi, int k) {
         if constexpr (VAR == kVarInt8) {
-            for (int kb = 0; kb < kbn; kb++) {
-                i32x4 fa[TM], fb[TN];
-                float dw[TN];
+            i32x4 fa[TM], fb[TN];
+            float dw[TN];
 #pragma unroll
-                for (int a = 0; a < TM; a++) {
-                    const int r = wm * (BM / 2) + a * 32 + (lane & 31);
-                    fa[a] = *reinterpret_cast<const i32x4 *>(&As[bi][r * ALD + kb * 32 + (lane >> 5) * 16]);
+            for (int a = 0; a < TM; a++) {
+                const int r = wm * (BM / 2) + a * 32 + (lane & 31);
+                fa[a] = *reinterpret_cast<const i32x4 *>(&As[bi][r * ALD + k * 32 + (lane >> 5) * 16]);
+            }
+#pragma unroll
+            for (int b = 0; b < TN; b++) {
+                const int c = wn * (BN / 2) + b * 32 + (lane & 31);
+                fb[b] = *reinterpret_cast<const i32x4 *>(&Bs[bi][c * BLD + k * 32 + (lane >> 5) * 16]);
+                dw[b] = Dw[bi][k][c];
+            }
+#pragma unroll
+            for (int a = 0; a < TM; a++) {
+                float sx[16];
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const f32x4 t = *reinterpret_cast<const f32x4 *>(&Sx[bi][k][wm * (BM / 2) + a * 32 + 8 * g + 4 * (lane >> 5)]);
+                    sx[4 * g] = t.x;
+                    sx[4 * g + 1] = t.y;
+                    sx[4 * g + 2] = t.z;
+                    sx[4 * g + 3] = t.w;
                 }
+                i32x16 I[TN];
 #pragma unroll
-                for (int b = 0; b < TN; b++) {
-                    const int c = wn * (BN / 2) + b * 32 + (lane & 31);
-                    fb[b] = *reinterpret_cast<const i32x4 *>(&Bs[bi][c * BLD + kb * 32 + (lane >> 5) * 16]);
-                    dw[b] = Dw[bi][kb][c];
-                }
+                for (int b = 0; b < TN; b++) I[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], i32x16{}, 0, 0, 0);
 #pragma unroll
-                for (int a = 0; a < TM; a++) {
-                    float sx[16];
+                for (int b = 0; b < TN; b++)
 #pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const f32x4 t = *reinterpret_cast<const f32x4 *>(&Sx[bi][kb][wm * (BM / 2) + a * 32 + 8 * g + 4 * (lane >> 5)]);
-                        sx[4 * g] = t.x;
-                        sx[4 * g + 1] = t.y;
-                        sx[4 * g + 2] = t.z;
-                        sx[4 * g + 3] = t.w;
-                    }
-#pragma unroll
-                    for (int b = 0; b < TN; b++) {
-                        const i32x16 zero = {};
-                        const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], zero, 0, 0, 0);
-#pragma unroll
-                        for (int v = 0; v < 16; v++)
-                            acc[a][b][v] = __builtin_fmaf((float)I[v], __fmul_rn(sx[v], dw[b]), acc[a][b][v]);
-                    }
-                }
+                    for (int v = 0; v < 16; v++)
+                        acc[a][b][v] = __builtin_fmaf((float)I[b][v], __fmul_rn(sx[v], dw[b]), acc[a][b][v]);
             }
         } else {
-            for (int ks = 0; ks < kbn * 2; ks++) {  // 16-element MFMA steps
-                bf16x8 fa[TM], fb[TN];
+            bf16x8 fa[TM], fb[TN];
 #pragma unroll
-                for (int a = 0; a < TM; a++) {
-                    const int r = wm * (BM / 2) + a * 32 + (lane & 31);
-                    fa[a] = *reinterpret_cast<const bf16x8 *>(&As[bi][r * ALD + ks * 32 + (lane >> 5) * 16]);
-                }
+            for (int a = 0; a < TM; a++) {
+                const int r = wm * (BM / 2) + a * 32 + (lane & 31);
+                fa[a] = *reinterpret_cast<const bf16x8 *>(&As[bi][r * ALD + k * 32 + (lane >> 5) * 16]);
+            }
+#pragma unroll
+            for (int b = 0; b < TN; b++) {
+                const int c = wn * (BN / 2) + b * 32 + (lane & 31);
+                fb[b] = *reinterpret_cast<const bf16x8 *>(&Bs[bi][c * BLD + k * 32 + (lane >> 5) * 16]);
+            }
+#pragma unroll
+            for (int a = 0; a < TM; a++)
 #pragma unroll
                 for (int b = 0; b < TN; b++) {
-                    const int c = wn * (BN / 2) + b * 32 + (lane & 31);
-                    fb[b] = *reinterpret_cast<const bf16x8 *>(&Bs[bi][c * BLD + ks * 32 + (lane >> 5) * 16]);
+                    f32x16 c;
+#pragma unroll
+                    for (int v = 0; v < 16; v++) c[v] = acc[a][b][v];
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], c, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[a][b][v] = c[v];
                 }
-#pragma unroll
-                for (int a = 0; a < TM; a++)
-#pragma unroll
-                    for (int b = 0; b < TN; b++) {
-                        f32x16 c;
-#pragma unroll
-                        for (int v = 0; v < 16; v++) c[v] = acc[a][b][v];
-                        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], c, 0, 0, 0);
-#pragma unroll
-                        for (int v = 0; v < 16; v++) acc[a][b][v] = c[v];
-                    }
-            }
         }
     };
+    constexpr int KS = VAR == kVarInt8 ? KB : 2 * KB;  // steps per stage; group g takes [g KS/G, (g+1) KS/G)
 
     // Issue the prologue sets in ring order (the scheduler may not interleave them): the wait
     // before each store then counts exactly the younger sets' loads.
@@ -314,22 +313,57 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
         load(r, set[r]);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // No early exit inside the ring: a stage past the end loads nothing (out-of-range
-    // offsets), stores zeros and computes no blocks. An exit here would make the wait
-    // before each store conservative (vmcnt(0)) and drain the ring every R stages.
+    store(set[0], 0);
+    // Iteration st: the barrier publishes stage st (stored during iteration st - 1) and frees
+    // the other buffer (its last reader, stage st - 1, is done); then the loads R stages ahead
+    // are issued, and stage st + 1 is dequantized/stored into the free buffer in the same
+    // basic block as stage st's MFMAs, so VALU, LDS and MFMA work interleave. No early exit
+    // inside the ring: a stage past the end loads nothing (out-of-range offsets) and computes
+    // no blocks; an exit would make the wait before each store conservative (vmcnt(0)).
     for (int base = 0; base < nst; base += R) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int st = base + r;
             const int bi = st & 1;
-            store(set[r], bi);
             __syncthreads();
             load(st + R, set[r]);
             __builtin_amdgcn_sched_barrier(0);
-            compute(st, bi);
+            if (nblk - st * KB >= KB) {
+                store(set[(r + 1) % R], bi ^ 1);
+#pragma unroll
+                for (int k = grp * KS / G; k < (grp + 1) * KS / G; k++) step(bi, k);
+            } else {
+                store(set[(r + 1) % R], bi ^ 1);
+                const int kn = (nblk - st * KB) * (KS / KB);  // steps of a partial (or empty) stage
+                for (int k = grp * KS / G; k < (grp + 1) * KS / G && k < kn; k++) step(bi, k);
+            }
         }
     }
 
+    if constexpr (G == 2) {
+        // group 1 hands its partial tile to group 0 through LDS (the stage buffers are free
+        // once every wave has passed this barrier); group 0 adds it in a fixed order
+        static_assert(4 * TM * TN * 16 * 64 * 4 <= (int)sizeof(As), "reduction scratch");
+        float *red = reinterpret_cast<float *>(&As[0][0]);
+        __syncthreads();
+        const int wq = wave & 3;
+        if (grp == 1) {
+#pragma unroll
+            for (int a = 0; a < TM; a++)
+#pragma unroll
+                for (int b = 0; b < TN; b++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) red[(((wq * TM + a) * TN + b) * 16 + v) * 64 + lane] = acc[a][b][v];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int a = 0; a < TM; a++)
+#pragma unroll
+            for (int b = 0; b < TN; b++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[a][b][v] += red[(((wq * TM + a) * TN + b) * 16 + v) * 64 + lane];
+    }
 #pragma unroll
     for (int a = 0; a < TM; a++)
 #pragma unroll
@@ -352,11 +386,11 @@ hipError_t launch_quantize_act(const uint16_t *x, int64_t m, int64_t k, int8_t *
     return hipGetLastError();
 }
 
-template <int VAR, int BM, int BN, int KB, int R>
+template <int VAR, int BM, int BN, int KB, int R, int G = 1>
 hipError_t launch_gemm(const QMat &w, const void *x, const float *xs, float *y, int64_t m, hipStream_t s) {
     const uint64_t tiles = (uint64_t)((w.rows + BN - 1) / BN) * (uint64_t)((m + BM - 1) / BM);
     if (tiles > 0x7fffffffu) return hipErrorInvalidValue;
-    gemm_kernel<VAR, BM, BN, KB, R><<<(unsigned)tiles, 256, 0, s>>>(w, x, xs, y, (int)m);
+    gemm_kernel<VAR, BM, BN, KB, R, G><<<(unsigned)tiles, 256 * G, 0, s>>>(w, x, xs, y, (int)m);
     return hipGetLastError();
 }
 
@@ -372,9 +406,9 @@ hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs,
 hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s) {
     if (m <= 0 || w.rows <= 0) return hipSuccess;
     if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols * 2 > 0x7fffffffull) return hipErrorInvalidValue;
-    if (m <= 64) return launch_gemm<kVarBf16, 64, 64, 4, 3>(w, x, nullptr, y, m, s);
-    if (m <= 512) return launch_gemm<kVarBf16, 128, 64, 2, 4>(w, x, nullptr, y, m, s);
-    return launch_gemm<kVarBf16, 128, 128, 2, 3>(w, x, nullptr, y, m, s);
+    if (m <= 64) return launch_gemm<kVarBf16, 64, 64, 4, 3, 2>(w, x, nullptr, y, m, s);
+    if (m <= 512) return launch_gemm<kVarBf16, 128, 64, 4, 3, 2>(w, x, nullptr, y, m, s);
+    return launch_gemm<kVarBf16, 128, 128, 2, 3, 1>(w, x, nullptr, y, m, s);
 }
 
 }  // namespace j4q
