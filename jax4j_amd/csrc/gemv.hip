@@ -1,6 +1,7 @@
 // Decode GEMV dispatch: picks the row-group size R, waves per workgroup and grid size of
 // the persistent GEMV kernel (gemv_impl.h) for each format and shape.
 #include "gemv_impl.h"
+#include "gemv_mfma.h"
 
 namespace j4q {
 
@@ -22,15 +23,43 @@ hipError_t launch_fmt(const QMat &m, const float *x, const float *add, float *y,
 
 int g_cus = 256;
 
-}  // namespace
+// Batched GEMV on the matrix cores (gemv_mfma.h) for up to 8 batch rows per launch:
+// persistent grid of one 8-wave workgroup per CU, K <= 4096 split into 8 wave slices of
+// 128 blocks / 8. Measured on MI355X (Q4_0 11008 x 4096): B = 4 11.8 us, B = 8 13.1 us,
+// against 22 us and 41 us for one vector-ALU pass per batch row; at B <= 2 the two are level.
+template <int FMT, int BB>
+hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
+    constexpr int IPW = FMT == Q8_0 ? 8 : 4;
+    const int tiles = (int)((m.rows + 15) / 16);
+    const int grid = tiles < g_cus ? tiles : g_cus;
+    return gmf::launch_k<FMT, BB, 8, IPW, false, 2>(m, x, add, y, b, grid, s);
+}
 
-void gemv_set_cus(int cus) { g_cus = cus > 0 ? cus : 256; }
+template <int FMT>
+hipError_t launch_mfma_fmt(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
+    return b <= 4 ? launch_mfma<FMT, 4>(m, x, add, y, b, s) : launch_mfma<FMT, 8>(m, x, add, y, b, s);
+}
 
-hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, float *y, int64_t batch,
-                       hipStream_t s) {
-    if (m.rows <= 0 || batch <= 0) return hipSuccess;
-    if (m.cols > gemv_max_cols() || batch > 65535 || m.rows > (1 << 30)) return hipErrorInvalidValue;
-    const int b = (int)batch;
+bool mfma_supported(int id, const QMat &m) {
+    const int64_t k = m.cols;
+    switch (id) {
+    case Q4_0: case Q4_K: case Q6_K: return k <= 4096 && k % 128 == 0;
+    case Q8_0: return k <= 4096 && k % 64 == 0;
+    default: return false;
+    }
+}
+
+hipError_t launch_mfma_any(int id, const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
+    switch (id) {
+    case Q4_0: return launch_mfma_fmt<Q4_0>(m, x, add, y, b, s);
+    case Q4_K: return launch_mfma_fmt<Q4_K>(m, x, add, y, b, s);
+    case Q6_K: return launch_mfma_fmt<Q6_K>(m, x, add, y, b, s);
+    case Q8_0: return launch_mfma_fmt<Q8_0>(m, x, add, y, b, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_valu(int id, const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
     switch (id) {
     case Q4_0: return launch_fmt<Q4_0>(m, x, add, y, b, g_cus, s);
     case Q8_0: return launch_fmt<Q8_0>(m, x, add, y, b, g_cus, s);
@@ -39,6 +68,30 @@ hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, 
     case Q2_0: return launch_fmt<Q2_0>(m, x, add, y, b, g_cus, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+}  // namespace
+
+void gemv_set_cus(int cus) { g_cus = cus > 0 ? cus : 256; }
+
+hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, float *y, int64_t batch,
+                       hipStream_t s) {
+    if (m.rows <= 0 || batch <= 0) return hipSuccess;
+    if (m.cols > gemv_max_cols() || batch > 65535 || m.rows > (1 << 30)) return hipErrorInvalidValue;
+    if (batch < 3 || !mfma_supported(id, m)) return launch_valu(id, m, x, add, y, (int)batch, s);
+    // batch rows in launches of up to 8 on the matrix cores; a remainder of 1 or 2 rows
+    // takes the vector-ALU kernel, which is as fast there
+    for (int64_t b0 = 0; b0 < batch;) {
+        const int64_t nb = batch - b0 < 8 ? batch - b0 : 8;
+        const float *xb = x + b0 * m.cols;
+        const float *ab = add ? add + b0 * m.rows : nullptr;
+        float *yb = y + b0 * m.rows;
+        const hipError_t e = nb >= 3 ? launch_mfma_any(id, m, xb, ab, yb, (int)nb, s)
+                                     : launch_valu(id, m, xb, ab, yb, (int)nb, s);
+        if (e != hipSuccess) return e;
+        b0 += nb;
+    }
+    return hipSuccess;
 }
 
 }  // namespace j4q

@@ -1,0 +1,535 @@
+// Batched decode GEMV on the matrix cores: y[b][n] = sum_k W[n, k] x[b][k] (+ add[b][n]) for
+// a batch of B <= 8 activation rows, split-layout weights, with W streamed once for the batch.
+//
+// The vector-ALU GEMV (gemv_impl.h) streams W once per batch row: at B = 8 it reads every
+// weight eight times. Here the products run on v_mfma_f32_16x16x32_f16 (16x16x16 for
+// Q6_K's 16-element scale groups), the A operand carries all batch rows at once, and the
+// VALU keeps only the unpack (5 bit operations per 8 Q4 weights) and one FMA per 32-block
+// per C row.
+//
+// Exactness of the operands:
+//  - Weights: a quant field AND-masked into the low bits of a 16-bit half is an fp16
+//    subnormal q * 2^-24 (16 q * 2^-24 for a field at bits 4..7). MFMA consumes fp16
+//    subnormals exactly, and products are exact in its fp32 accumulator.
+//  - Activations: per batch row and wave, x is scaled by a power of two 2^e (max |x| * 2^e
+//    over the wave's K slice in [2^14, 2^15), so nothing overflows fp16) and split into
+//    x' = hi + lo, two fp16 values carrying 22 significant bits. The A operand's 16 rows
+//    hold hi of batch rows 0..7 (rows 0..7) and lo (rows 8..15); rows without a batch row
+//    are zero. A wave's partial sums are multiplied by 2^(24 - e) before the waves' sums
+//    are added, so each wave may pick its own e.
+//  - Offsets: the MFMA's C input carries -OFF * 2^-24 * sum(x') of the block, so the C
+//    output is 2^-24 * sum (q - OFF) x' and one FMA with the block scale folds it into
+//    the fp32 accumulator (Q4_K's min term is a second FMA).
+//
+// Work split: persistent workgroups take 16-row tiles; wave v of a workgroup owns a fixed K
+// slice of IPW items (an item is 16 rows x 4 blocks; Q8_0: 2 blocks) for every tile, so it
+// turns its slice of x into MFMA operands once. Lane l = 16 g + n loads 16 contiguous bytes
+// of row n, unit g of the item; a 4 x 4 transpose across the 16-lane groups
+// (v_permlane32_swap / v_permlane16_swap) leaves lane group g holding dword g of every
+// unit, so each MFMA column sums one block of one row. The waves' partial sums of a tile are
+// added through LDS in wave order, so results are deterministic. Two tiles' loads are in
+// flight while a tile is computed.
+#pragma once
+
+#include "gemv_impl.h"
+
+namespace j4q {
+namespace gmf {
+
+using gemv::f32x4;
+using gemv::kOob;
+using gemv::kStream;
+using gemv::ld128;
+using gemv::ld64;
+using gemv::make_rsrc;
+using gemv::Rsrc;
+using gemv::u32x2;
+using gemv::u32x4;
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, kStream);
+}
+
+// On entry lane group g (lanes 16g..16g+15) holds v[0..3] = dwords 0..3 of its own unit g;
+// on exit v[t] holds dword g of unit t.
+__device__ __forceinline__ void xpose4(uint32_t (&v)[4]) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    v[0] = c[0];
+    v[1] = c[1];
+    v[2] = d[0];
+    v[3] = d[1];
+}
+
+// Q4 dword of lane group g: bytes 4g..4g+3 of a 16-byte chunk (byte i: lo nibble element
+// i, hi nibble element 16 + i). Slots 0..7 of the B operand hold elements
+// 4g + {0, 2, 1, 3, 16, 18, 17, 19}; slots 4..7 carry a factor 16.
+__device__ __forceinline__ u32x4 q4_slots(uint32_t v) {
+    const uint32_t t = v >> 8;
+    return u32x4{v & 0x000F000Fu, t & 0x000F000Fu, v & 0x00F000F0u, t & 0x00F000F0u};
+}
+
+template <int FMT>
+struct Fmt;
+
+// Geometry shared by the formats: S blocks (32-element units) per item, the x scale of
+// slots 4..7 (Q4-style fields sit at bits 4..7), and the per-block offset of the quants.
+template <>
+struct Fmt<Q4_0> {
+    static constexpr int S = 4, GROUPS = 1;
+    static constexpr float SIGMA = 0.0625f, OFF = 8.0f;
+    u32x4 q;
+    u32x2 d;  // unused: the tile's scales are loaded once per tile (see load_tile)
+    __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
+        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob;
+        q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
+    }
+};
+
+template <>
+struct Fmt<Q4_K> {
+    static constexpr int S = 4, GROUPS = 1;
+    static constexpr float SIGMA = 0.0625f, OFF = 0.0f;
+    u32x4 q;
+    u32x4 meta;  // superblock: d | dmin | D0 | D1 | D2 (split layout, j4q_common.h)
+    __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
+        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob, so_s = live ? (uint32_t)(blk0 >> 3) * 16u : kOob;
+        q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
+        meta = ld128(r.sc, row * (K / 16u), so_s);
+    }
+};
+
+template <>
+struct Fmt<Q8_0> {
+    static constexpr int S = 2, GROUPS = 1;
+    static constexpr float SIGMA = 1.0f, OFF = 128.0f;
+    u32x4 q;
+    uint32_t d;  // fp16 d of blocks 0..1
+    __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
+        const uint32_t so_q = live ? (uint32_t)blk0 * 32u : kOob, so_s = live ? (uint32_t)blk0 * 2u : kOob;
+        q = ld128(r.qs, row * K + 16u * g, so_q);
+        d = ld32(r.sc, row * (K / 16u), so_s);
+    }
+};
+
+template <>
+struct Fmt<Q6_K> {
+    static constexpr int S = 4, GROUPS = 2;
+    static constexpr float SIGMA = 0.0625f, OFF = 32.0f;
+    u32x4 q;
+    u32x2 h;   // qh of chunk g (two dwords)
+    u32x2 sc;  // int8 group scales of chunks 0..3
+    uint32_t d;
+    __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
+        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob;
+        const uint32_t so_h = live ? (uint32_t)blk0 * 8u : kOob;
+        const uint32_t so_s = live ? (uint32_t)blk0 * 2u : kOob;
+        const uint32_t so_d = live ? (uint32_t)(blk0 >> 3) * 2u : kOob;
+        q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
+        h = ld64(r.qh, row * (K / 4u) + 8u * g, so_h);
+        sc = ld64(r.sc, row * (K / 16u), so_s);
+        d = gemv::ld16(r.d, row * (K / 128u), so_d);
+    }
+};
+
+// LDS plan for BB batch rows, WAVES waves of NBW blocks each (byte offsets):
+//   xa   [WAVES * NBW][2 BB rows][4 lane groups][16 B]   hi/lo fp16 x image
+//   zero 512 BB bytes of zeros (A rows with no batch row read here, stride 0)
+//   cin  [WAVES * NBW][G][BB] f32                         MFMA C input per block
+//   part [2][WAVES][BB][16] f32                           per-wave partial sums
+template <int BB, int G, int WAVES, int NBW>
+struct Plan {
+    static constexpr int kXa = 0;
+    static constexpr int kZero = kXa + WAVES * NBW * 128 * BB;
+    static constexpr int kCin = kZero + 512 * BB;
+    static constexpr int kPart = kCin + WAVES * NBW * G * BB * 4;
+    static constexpr int kBytes = kPart + 2 * WAVES * BB * 16 * 4;
+};
+
+// grid: G_wg persistent workgroups of WAVES waves; workgroup w takes 16-row tiles w,
+// w + G_wg, ... Wave v owns blocks [v NBW, (v + 1) NBW) of K (NBW = IPW * S); blocks past
+// K / 32 load nothing and their x image is zero. Requires K % (32 S) == 0,
+// K <= WAVES * NBW * 32 and B <= BB. XREG keeps the wave's A operands and C inputs in
+// registers for the whole kernel instead of re-reading them from LDS per tile.
+template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS>
+__global__ void __launch_bounds__(WAVES * 64)
+gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, float *__restrict__ y, int B) {
+    using F = Fmt<FMT>;
+    constexpr int S = F::S, G = F::GROUPS, NBW = IPW * S;
+    using P = Plan<BB, G, WAVES, NBW>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int K = (int)m.cols, N = (int)m.rows;
+    const int tiles = (N + 15) / 16, nb = K / 32;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int blkw = wave * NBW;  // first block of this wave's K slice
+    const Rsrc rs = gemv::rsrc_of(m, FMT);
+
+    // ---- 1. x image of this wave's slice, built before any weight load is issued --------
+    // Weight loads block at issue once the memory queues are full; anything queued behind
+    // them in a wave (such as this prologue) would wait for the whole stream. So each wave
+    // first turns its own slice of x into MFMA operands, with its own power-of-two scale per
+    // batch row (applied again when its partial sums are written), and needs no barrier.
+    constexpr int UNITS = BB * 4;                 // (batch row, lane group) units per block
+    constexpr int XPL = (NBW * UNITS + 63) / 64;  // units per lane
+    f32x4 xv[XPL][2];
+    {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint64_t)B * (uint64_t)K * 4u);
+#pragma unroll
+        for (int i = 0; i < XPL; i++) {
+            const int u = lane + 64 * i;
+            const int bl = u / UNITS, rem = u - bl * UNITS, b = rem >> 2, gg = rem & 3;
+            const bool ok = u < NBW * UNITS && b < B && blkw + bl < nb;
+            const uint32_t off = (uint32_t)(b * K + (blkw + bl) * 32 + 4 * gg) * 4u;
+            xv[i][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? off : kOob, 0, 0));
+            xv[i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? off + 64u : kOob, 0, 0));
+        }
+    }
+    // zero block for the A rows and C inputs that carry no batch row (every wave writes the
+    // same zeros, so no wave depends on another)
+    for (int i = lane; i < 128 * BB; i += 64) reinterpret_cast<uint32_t *>(lds + P::kZero)[i] = 0u;
+    float sx[BB];
+    int ex[BB];
+    {
+        float mx[BB];
+#pragma unroll
+        for (int b = 0; b < BB; b++) mx[b] = 0.f;
+#pragma unroll
+        for (int i = 0; i < XPL; i++) {
+            const int b = ((lane + 64 * i) % UNITS) >> 2;
+            const f32x4 a = xv[i][0], c = xv[i][1];
+            const float v = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                  fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))));
+#pragma unroll
+            for (int bb = 0; bb < BB; bb++) mx[bb] = (b == bb) ? fmaxf(mx[bb], v) : mx[bb];
+        }
+#pragma unroll
+        for (int bb = 0; bb < BB; bb++) {
+            float v = mx[bb];
+            v = fmaxf(v, gemv::dpp<0xB1>(v));
+            v = fmaxf(v, gemv::dpp<0x4E>(v));
+            v = fmaxf(v, gemv::dpp<0x141>(v));
+            v = fmaxf(v, gemv::dpp<0x140>(v));
+            v = fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)),
+                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16))),
+                      fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)),
+                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48))));
+            // 2^e brings the slice maximum into [2^14, 2^15): no fp16 overflow, full precision
+            int e = 0;
+            if (v > 0.f && v <= 3.402823466e38f) {
+                int E;
+                (void)frexpf(v, &E);
+                e = 15 - E;
+                e = e < -126 ? -126 : (e > 127 ? 127 : e);
+            }
+            ex[bb] = e;
+            sx[bb] = ldexpf(1.0f, e);
+        }
+    }
+    {
+        uint8_t *xa = lds + P::kXa;
+        float *cin = reinterpret_cast<float *>(lds + P::kCin);
+#pragma unroll
+        for (int i = 0; i < XPL; i++) {
+            const int u = lane + 64 * i;
+            const int bl = u / UNITS, rem = u - bl * UNITS, b = rem >> 2, gg = rem & 3;
+            const int blk = blkw + bl;
+            float s = 0.f;
+#pragma unroll
+            for (int bb = 0; bb < BB; bb++) s = (b == bb) ? sx[bb] : s;
+            const f32x4 a = xv[i][0] * s, c = xv[i][1] * s;
+            const f32x4 hi4 = c * F::SIGMA;
+            // slots: 4g + {0, 2, 1, 3}, then 16 + 4g + {0, 2, 1, 3} times SIGMA
+            const float v[8] = {a.x, a.z, a.y, a.w, hi4.x, hi4.z, hi4.y, hi4.w};
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const h2 h = __builtin_convertvector((f32x2{v[2 * p], v[2 * p + 1]}), h2);
+                const float r0 = v[2 * p] - (float)h.x, r1 = v[2 * p + 1] - (float)h.y;
+                const h2 l = __builtin_convertvector((f32x2{r0, r1}), h2);
+                hw[p] = __builtin_bit_cast(uint32_t, h);
+                lw[p] = __builtin_bit_cast(uint32_t, l);
+            }
+            // block sums of x' over elements 0..15 and 16..31 (this unit's 4 + 4, then the quad)
+            float s0 = (a.x + a.y) + (a.z + a.w), s1 = (c.x + c.y) + (c.z + c.w);
+            s0 += gemv::dpp<0xB1>(s0);
+            s0 += gemv::dpp<0x4E>(s0);
+            s1 += gemv::dpp<0xB1>(s1);
+            s1 += gemv::dpp<0x4E>(s1);
+            if (u < NBW * UNITS) {
+                *reinterpret_cast<u32x4 *>(xa + ((blk * 2 * BB + b) * 4 + gg) * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4 *>(xa + ((blk * 2 * BB + BB + b) * 4 + gg) * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                if (gg == 0) {
+                    constexpr float U = 5.9604644775390625e-8f;  // 2^-24
+                    if constexpr (G == 2) {
+                        cin[(blk * 2 + 0) * BB + b] = -F::OFF * U * s0;
+                        cin[(blk * 2 + 1) * BB + b] = -F::OFF * U * s1;
+                    } else if constexpr (FMT == Q4_K) {
+                        cin[blk * BB + b] = U * (s0 + s1);
+                    } else {
+                        cin[blk * BB + b] = -F::OFF * U * (s0 + s1);
+                    }
+                }
+            }
+        }
+    }
+    // The slice was written by this wave only; LDS operations of one wave complete in order,
+    // so waiting for them is all the ordering the reads below need.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+
+    // Lane (m, g) of the A operand: rows m < BB are hi of batch row m, rows 8..8+BB-1 lo of
+    // batch row m - 8, other rows read the zero block with stride 0. The C rows of lane
+    // group g are 4g..4g+3: groups 0 and 1 hold the hi rows of batch rows 4 (g & 1) + j and
+    // take the C inputs; groups 2 and 3 hold the lo rows and read zeros.
+    const int mrow = lane & 15;
+    int abase, astride;
+    if (mrow < BB) {
+        abase = P::kXa + ((blkw * 2 * BB + mrow) * 4 + g) * 16;
+        astride = 128 * BB;
+    } else if (mrow >= 8 && mrow < 8 + BB) {
+        abase = P::kXa + ((blkw * 2 * BB + BB + mrow - 8) * 4 + g) * 16;
+        astride = 128 * BB;
+    } else {
+        abase = P::kZero + g * 16;
+        astride = 0;
+    }
+    constexpr int JB = BB < 4 ? BB : 4;  // C rows per lane that carry a batch row
+    const int hb = 4 * (g & 1);          // first batch row of this lane's C rows
+    const bool hi_lane = g < 2 && hb < BB;
+    const int cbase = hi_lane ? P::kCin + (blkw * G * BB + hb) * 4 : P::kZero;
+    const int cstride = hi_lane ? G * BB * 4 : 0;
+    auto a_op = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + bl * astride); };
+    auto c_in = [&](int bl, int k) { return reinterpret_cast<const float *>(lds + cbase + bl * cstride)[k]; };
+    // registers keep only this lane's C inputs: k = j (group 0) and k = BB + j (Q6_K group 1)
+    h8 areg[XREG ? NBW : 1];
+    float creg[XREG ? NBW : 1][G * JB];
+    if constexpr (XREG) {
+#pragma unroll
+        for (int bl = 0; bl < NBW; bl++) {
+            areg[bl] = a_op(bl);
+#pragma unroll
+            for (int kk = 0; kk < G * JB; kk++) creg[bl][kk] = c_in(bl, kk < JB ? kk : BB + kk - JB);
+        }
+    }
+
+    // ---- 2. weight loads of the first two tiles -----------------------------------------
+    // The reducing threads (b, nn) = (tid / 16, tid % 16), tid < 16 BB, also fetch add[b][row]
+    // with the tile's weights, so waiting for it never drains the loads issued later.
+    const __amdgpu_buffer_rsrc_t addr = make_rsrc(add ? (const void *)add : (const void *)y, add ? (uint64_t)B * N * 4u : 0);
+    const int rb = (int)threadIdx.x >> 4, rn = (int)threadIdx.x & 15;
+    // Q4_0 scales: one load per tile, lane group g fetching item g's four (16 rows x 32 B
+    // instead of 16 rows x 8 B per item); process() broadcasts them across the groups.
+    static_assert(FMT != Q4_0 || IPW <= 4, "Q4_0 tile scales cover four items");
+    auto load_tile = [&](F (&it)[IPW], float &av, int tile) {
+        const bool live = tile < tiles;
+        const int r = tile * 16 + n;
+        const uint32_t row = (uint32_t)(r < N ? r : N - 1);
+#pragma unroll
+        for (int i = 0; i < IPW; i++)
+            it[i].load(rs, row, (uint32_t)K, (uint32_t)g, blkw + i * S, live && blkw + i * S < nb);
+        if constexpr (FMT == Q4_0) {
+            const bool ok = live && g < IPW && blkw + g * S < nb;
+            it[0].d = ld64(rs.sc, row * (uint32_t)(K / 16) + 8u * (uint32_t)g, ok ? (uint32_t)blkw * 2u : kOob);
+        }
+        const int ar = tile * 16 + rn;
+        const bool aok = live && (int)threadIdx.x < 16 * BB && rb < B && ar < N;
+        av = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(addr, aok ? (uint32_t)(rb * N + ar) * 4u : kOob, 0, 0));
+    };
+    F ta[IPW], tb[TS == 2 ? IPW : 1];
+    float aa, ab;
+    const int t0 = (int)blockIdx.x, tstep = (int)gridDim.x;
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(ta, aa, t0);
+    if constexpr (TS == 2) load_tile(tb, ab, t0 + tstep);
+    __builtin_amdgcn_sched_barrier(0);
+    // per-batch-row factor that undoes this wave's x scale and the 2^-24 of the weights
+    float wscale[BB];
+#pragma unroll
+    for (int bb = 0; bb < BB; bb++) wscale[bb] = ldexpf(1.0f, 24 - ex[bb]);
+
+    auto A = [&](int bl) -> h8 {
+        if constexpr (XREG) return areg[bl];
+        else return a_op(bl);
+    };
+    auto C = [&](int bl, int k) -> float {
+        if constexpr (XREG) return creg[bl][k < BB ? k : JB + k - BB];
+        else return c_in(bl, k);
+    };
+
+    // ---- 3. per tile: transpose, unpack, MFMA, block scale; partials through LDS ----------
+    float *part = reinterpret_cast<float *>(lds + P::kPart);
+    auto process = [&](const F (&it)[IPW], float av, int tile, int parity) {
+        float acc[JB], corr[JB];
+#pragma unroll
+        for (int j = 0; j < JB; j++) acc[j] = corr[j] = 0.f;
+        // Q4_0: item i's scales live in lane group i of it[0].d; broadcast them to all groups
+        uint32_t bd[4][2];
+        if constexpr (FMT == Q4_0) {
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                const uint32_t v = w ? it[0].d.y : it[0].d.x;
+                const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // [g0 g1 g0 g1], [g2 g3 g2 g3]
+                const auto b0 = __builtin_amdgcn_permlane16_swap(a[0], a[0], false, false);
+                const auto b1 = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);
+                bd[0][w] = b0[0];
+                bd[1][w] = b0[1];
+                bd[2][w] = b1[0];
+                bd[3][w] = b1[1];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < IPW; i++) {
+            const int blk0 = blkw + i * S;
+            if constexpr (FMT == Q4_0 || FMT == Q4_K) {
+                uint32_t v[4] = {it[i].q.x, it[i].q.y, it[i].q.z, it[i].q.w};
+                xpose4(v);
+                f32x4 c[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int bl = i * S + t;
+                    c[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (FMT == Q4_0) {
+#pragma unroll
+                        for (int j = 0; j < JB; j++) c[t][j] = C(bl, j);
+                    }
+                    c[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A(bl), __builtin_bit_cast(h8, q4_slots(v[t])), c[t], 0, 0, 0);
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int bl = i * S + t;
+                    if constexpr (FMT == Q4_0) {
+                        const uint32_t dw = bd[i][t >> 1];
+                        const float df = (float)__builtin_bit_cast(h2, dw)[t & 1];
+#pragma unroll
+                        for (int j = 0; j < JB; j++) acc[j] = __builtin_fmaf(df, c[t][j], acc[j]);
+                    } else {
+                        const u32x4 mt = it[i].meta;
+                        const int sj = (blk0 & 7) + t;
+                        const float dd = (float)__builtin_bit_cast(h2, mt.x)[0];
+                        const float dm = (float)__builtin_bit_cast(h2, mt.x)[1];
+                        const uint32_t scj = __builtin_amdgcn_ubfe(mt.y, 4 * sj, 4) | (__builtin_amdgcn_ubfe(mt.w, 2 * sj, 2) << 4);
+                        const uint32_t mnj = __builtin_amdgcn_ubfe(mt.z, 4 * sj, 4) | (__builtin_amdgcn_ubfe(mt.w, 16 + 2 * sj, 2) << 4);
+                        const float dsc = dd * (float)scj, dmn = dm * (float)mnj;
+#pragma unroll
+                        for (int j = 0; j < JB; j++) {
+                            acc[j] = __builtin_fmaf(dsc, c[t][j], acc[j]);
+                            corr[j] = __builtin_fmaf(dmn, C(bl, j), corr[j]);
+                        }
+                    }
+                }
+            } else if constexpr (FMT == Q8_0) {
+                uint32_t v[4] = {it[i].q.x, it[i].q.y, it[i].q.z, it[i].q.w};
+                xpose4(v);
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const int bl = i * S + t;
+                    const uint32_t ua = v[2 * t] ^ 0x80808080u, ub = v[2 * t + 1] ^ 0x80808080u;
+                    const u32x4 sl = {ua & 0x00FF00FFu, (ua >> 8) & 0x00FF00FFu, ub & 0x00FF00FFu, (ub >> 8) & 0x00FF00FFu};
+                    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < JB; j++) c[j] = C(bl, j);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A(bl), __builtin_bit_cast(h8, sl), c, 0, 0, 0);
+                    const float df = (float)__builtin_bit_cast(h2, it[i].d)[t];
+#pragma unroll
+                    for (int j = 0; j < JB; j++) acc[j] = __builtin_fmaf(df, c[j], acc[j]);
+                }
+            } else {  // Q6_K
+                uint32_t v[4] = {it[i].q.x, it[i].q.y, it[i].q.z, it[i].q.w};
+                xpose4(v);
+                // qh: lane group g holds dwords {0, 1} of chunk g; chunk t needs dword g >> 1
+                // of chunk t, rotated right by 8 when g is odd.
+                const auto hs = __builtin_amdgcn_permlane32_swap(it[i].h.x, it[i].h.y, false, false);
+                const auto e0 = __builtin_amdgcn_permlane16_swap(hs[0], hs[0], false, false);
+                const auto e1 = __builtin_amdgcn_permlane16_swap(hs[1], hs[1], false, false);
+                const uint32_t hq[4] = {e0[0], e0[1], e1[0], e1[1]};
+                const float df = (float)__builtin_bit_cast(_Float16, (uint16_t)(it[i].d & 0xFFFFu));
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int bl = i * S + t;
+                    const uint32_t q = v[t];
+                    const uint32_t hw = __builtin_amdgcn_alignbit(hq[t], hq[t], (uint32_t)(g & 1) * 8u);
+                    const uint32_t tq = q >> 8, hsh = hw >> 2;
+                    const uint32_t p0 = (q & 0x000F000Fu) | (hw & 0x00300030u);
+                    const uint32_t p1 = (q & 0x00F000F0u) | (hw & 0x03000300u);
+                    const uint32_t p2 = (tq & 0x000F000Fu) | (hsh & 0x00300030u);
+                    const uint32_t p3 = (tq & 0x00F000F0u) | (hsh & 0x03000300u);
+                    const h8 aop = A(bl);
+                    f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < JB; j++) {
+                        c0[j] = C(bl, j);
+                        c1[j] = C(bl, BB + j);
+                    }
+                    c0 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(aop, aop, 0, 1, 2, 3),
+                                                               __builtin_bit_cast(h4, u32x2{p0, p2}), c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(aop, aop, 4, 5, 6, 7),
+                                                               __builtin_bit_cast(h4, u32x2{p1, p3}), c1, 0, 0, 0);
+                    const uint32_t scw = t < 2 ? it[i].sc.x : it[i].sc.y;
+                    const float s0 = df * (float)(int8_t)(scw >> (16 * (t & 1))),
+                                s1 = df * (float)(int8_t)(scw >> (16 * (t & 1) + 8));
+#pragma unroll
+                    for (int j = 0; j < JB; j++) acc[j] = __builtin_fmaf(s1, c1[j], __builtin_fmaf(s0, c0[j], acc[j]));
+                }
+            }
+        }
+        // hi + lo (lanes 32..63 hold the lo rows of the batch rows in lanes 0..31)
+        float *pp = part + parity * (WAVES * BB * 16);
+#pragma unroll
+        for (int j = 0; j < JB; j++) {
+            float v = acc[j] - corr[j];
+            const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                             __builtin_bit_cast(uint32_t, v), false, false);
+            v += __builtin_bit_cast(float, (uint32_t)sw[1]);
+            float ws = 0.f;
+#pragma unroll
+            for (int bb = 0; bb < BB; bb++) ws = (bb == hb + j) ? wscale[bb] : ws;
+            if (hi_lane) pp[(wave * BB + hb + j) * 16 + n] = v * ws;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < BB * 16) {
+            float s = 0.f;
+            for (int w = 0; w < WAVES; w++) s += pp[(w * BB + rb) * 16 + rn];
+            const int r = tile * 16 + rn;
+            if (rb < B && r < N) y[(int64_t)rb * N + r] = add ? s + av : s;
+        }
+    };
+
+    // Two register sets alternate: the next tile's loads are in flight while a tile is
+    // computed and reduced. The tile loop is workgroup-uniform, so every wave reaches each
+    // barrier.
+    if constexpr (TS == 2) {
+        for (int t = t0; t < tiles; t += 2 * tstep) {
+            process(ta, aa, t, 0);
+            load_tile(ta, aa, t + 2 * tstep);
+            if (t + tstep >= tiles) break;
+            process(tb, ab, t + tstep, 1);
+            load_tile(tb, ab, t + 3 * tstep);
+        }
+    } else {
+        for (int t = t0; t < tiles; t += 2 * tstep) {
+            process(ta, aa, t, 0);
+            if (t + tstep >= tiles) break;
+            load_tile(ta, aa, t + tstep);
+            process(ta, aa, t + tstep, 1);
+            load_tile(ta, aa, t + 2 * tstep);
+        }
+    }
+}
+
+template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS = 2>
+hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, int B, int grid, hipStream_t s) {
+    constexpr int NBW = IPW * Fmt<FMT>::S;
+    constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW>::kBytes;
+    gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<grid, WAVES * 64, lds, s>>>(m, x, add, y, B);
+    return hipGetLastError();
+}
+
+}  // namespace gmf
+}  // namespace j4q

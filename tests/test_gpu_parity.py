@@ -179,9 +179,91 @@ def test_gemv_add_and_batch(backend, uploaded, qt):
     yb = backend.quant_matvec(w, xbb)
     assert yb.shape == (B, rows)
     got = backend.download(yb).reshape(B, rows)
-    assert np.array_equal(bits(got), bits(np.stack(singles)))
+    # B >= 3 may run on the matrix cores (a different fp32 summation order than B = 1)
+    for b in range(B):
+        assert rel_err(got[b], singles[b].astype(np.float64)) <= 1e-5
+        assert rel_err(got[b], oracle.matvec_f64(qt.id, blob, rows, cols, xs[b])) <= TOL
     backend.release(yb)
     backend.release(xbb)
+
+
+# Batched GEMV shapes the matrix-core kernel takes (K <= 4096, K % 128 == 0), plus the
+# benchmark's batch-8 Q4_0 shape; rows not a multiple of 16 exercise the last tile.
+BATCH_CASES = [
+    (QuantType.Q4_0, 300, 1024), (QuantType.Q4_0, 11008, 4096),
+    (QuantType.Q8_0, 300, 1024), (QuantType.Q8_0, 4096, 4096),
+    (QuantType.Q4_K, 300, 2304), (QuantType.Q4_K, 1024, 4096),
+    (QuantType.Q6_K, 300, 2304), (QuantType.Q6_K, 2000, 4096),
+]
+
+
+@pytest.mark.parametrize("qt,rows,cols", BATCH_CASES, ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [3, 8, 9, 16])
+def test_gemv_batched_matches_oracle(backend, uploaded, qt, rows, cols, B):
+    note("batched", qt.name, rows, cols, "B", B)
+    blob, w = uploaded(qt, rows, cols)
+    xs = S.activations_f32(rows + 7 * B, B * cols).reshape(B, cols)
+    add = S.activations_f32(rows + 5, B * rows).reshape(B, rows)
+    xb = backend.upload(xs, shape=(B, cols))
+    ab = backend.upload(add, shape=(B, rows))
+    y = backend.quant_matvec(w, xb)
+    ya = backend.quant_matvec_add(w, xb, ab)
+    got = backend.download(y).reshape(B, rows)
+    gota = backend.download(ya).reshape(B, rows)
+    for b in range(B):
+        y64 = oracle.matvec_f64(qt.id, blob, rows, cols, xs[b])
+        assert rel_err(got[b], y64) <= TOL, f"row {b}"
+        assert rel_err(got[b], y64) <= 1e-5, f"row {b}"
+    # quantMatvecAdd rounds the add on its own
+    assert np.array_equal(bits(gota), bits(got + add))
+    # each batch row depends on its own x only: a permuted batch gives the permuted rows.
+    # Rows are launched in groups of 8 (a remainder of 1-2 rows takes the vector-ALU
+    # kernel, which sums in another order), so the permutation stays inside each group.
+    perm = np.arange(B)
+    for c in range(0, B, 8):
+        if min(B, c + 8) - c >= 3:
+            perm[c:c + 8] = np.roll(perm[c:c + 8], 1)
+    xp = backend.upload(np.ascontiguousarray(xs[perm]), shape=(B, cols))
+    yp = backend.quant_matvec(w, xp)
+    assert np.array_equal(bits(backend.download(yp).reshape(B, rows)), bits(got[perm]))
+    # scaling x by 2 scales every product and partial sum exactly
+    x2 = backend.upload(2.0 * xs, shape=(B, cols))
+    y2 = backend.quant_matvec(w, x2)
+    assert np.array_equal(bits(backend.download(y2).reshape(B, rows)), bits(2.0 * got))
+    for h in (xb, ab, y, ya, xp, yp, x2, y2):
+        backend.release(h)
+
+
+@pytest.mark.parametrize("qt", [QuantType.Q4_0, QuantType.Q8_0, QuantType.Q4_K, QuantType.Q6_K], ids=lambda q: q.name)
+def test_gemv_batched_one_hot_and_range(backend, uploaded, qt):
+    rows, cols = (300, 2304) if qt in (QuantType.Q4_K, QuantType.Q6_K) else (300, 1024)
+    note("batched onehot/range", qt.name, rows, cols)
+    blob, w = uploaded(qt, rows, cols)
+    wd = oracle.dequant_matrix(qt.id, blob, rows, cols)
+    B = 5
+    js = [0, 31, cols // 2 + 3, cols - 1, 17]
+    xs = np.zeros((B, cols), np.float32)
+    for b, j in enumerate(js):
+        xs[b, j] = 1.0
+    xb = backend.upload(xs, shape=(B, cols))
+    y = backend.quant_matvec(w, xb)
+    got = backend.download(y).reshape(B, rows)
+    for b, j in enumerate(js):
+        assert np.array_equal(got[b], wd[:, j]), f"column {j}"
+    backend.release(y)
+    backend.release(xb)
+    # x far outside fp16 range, and far below it: the per-row power-of-two scale keeps the
+    # hi/lo split exact to 22 bits either way
+    xs = S.activations_f32(4242, B * cols).reshape(B, cols)
+    scales = np.array([1e30, 1e-30, 1.0, 3e4, 1e-6], np.float32)
+    xr = (xs * scales[:, None]).astype(np.float32)
+    xb = backend.upload(xr, shape=(B, cols))
+    y = backend.quant_matvec(w, xb)
+    got = backend.download(y).reshape(B, rows)
+    for b in range(B):
+        assert rel_err(got[b], oracle.matvec_f64(qt.id, blob, rows, cols, xr[b])) <= 1e-5, f"scale {scales[b]}"
+    backend.release(y)
+    backend.release(xb)
 
 
 def test_shape_and_index_errors(backend, uploaded):
