@@ -61,6 +61,12 @@ class Hip:
             "hipEventRecord": [C.c_void_p, C.c_void_p],
             "hipEventSynchronize": [C.c_void_p],
             "hipEventElapsedTime": [C.POINTER(C.c_float), C.c_void_p, C.c_void_p],
+            "hipStreamBeginCapture": [C.c_void_p, C.c_int],
+            "hipStreamEndCapture": [C.c_void_p, C.POINTER(C.c_void_p)],
+            "hipGraphInstantiate": [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
+            "hipGraphLaunch": [C.c_void_p, C.c_void_p],
+            "hipGraphExecDestroy": [C.c_void_p],
+            "hipGraphDestroy": [C.c_void_p],
         }.items():
             fn = getattr(self.h, name)
             fn.argtypes = args
@@ -88,6 +94,25 @@ class Hip:
 
     def record(self, e: int, stream: int) -> None:
         self.ok(self.h.hipEventRecord(C.c_void_p(e), C.c_void_p(stream)), "hipEventRecord")
+
+    def capture(self, stream: int, enqueue):
+        """A graph of everything `enqueue()` puts on `stream` (relaxed capture mode)."""
+        self.ok(self.h.hipStreamBeginCapture(C.c_void_p(stream), 2), "hipStreamBeginCapture")
+        try:
+            enqueue()
+        finally:
+            g = C.c_void_p()
+            self.ok(self.h.hipStreamEndCapture(C.c_void_p(stream), C.byref(g)), "hipStreamEndCapture")
+        ex = C.c_void_p()
+        self.ok(self.h.hipGraphInstantiate(C.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        return ex.value, g.value
+
+    def graph_launch(self, exec_: int, stream: int) -> None:
+        self.ok(self.h.hipGraphLaunch(C.c_void_p(exec_), C.c_void_p(stream)), "hipGraphLaunch")
+
+    def graph_free(self, exec_: int, graph: int) -> None:
+        self.ok(self.h.hipGraphExecDestroy(C.c_void_p(exec_)), "hipGraphExecDestroy")
+        self.ok(self.h.hipGraphDestroy(C.c_void_p(graph)), "hipGraphDestroy")
 
     def elapsed_ms(self, a: int, b: int) -> float:
         self.ok(self.h.hipEventSynchronize(C.c_void_p(b)), "hipEventSynchronize")
@@ -189,12 +214,20 @@ def gemv_workload(eng: Engine, name: str, qt: QuantType, rows: int, cols: int, b
     }
 
 
-def decode_workload(eng: Engine, batch: int, steps: int, warmup: int, layers: int = 32):
+def decode_workload(eng: Engine, batch: int, steps: int, warmup: int, layers: int = 32, fused: bool = False,
+                    graph: bool = False):
     """Synthetic Llama-3-8B decode step, matmuls only (Q4_K_M mix): 32 x (q, k, v, o, gate,
-    up: Q4_K; down: Q6_K) + a 128256 x 4096 Q6_K head = 225 GEMVs per step."""
-    shapes = [(QuantType.Q4_K, 4096, 4096), (QuantType.Q4_K, 1024, 4096), (QuantType.Q4_K, 1024, 4096),
-              (QuantType.Q4_K, 4096, 4096), (QuantType.Q4_K, 14336, 4096), (QuantType.Q4_K, 14336, 4096),
-              (QuantType.Q6_K, 4096, 14336)]
+    up: Q4_K; down: Q6_K) + a 128256 x 4096 Q6_K head = 225 GEMVs per step. With `fused`,
+    the matrices that share an input run as one (q|k|v 6144 x 4096, gate|up 28672 x 4096, the
+    rows concatenated as j4q_concat_rows does at load time): 129 launches streaming the same
+    bytes. With `graph`, one step is captured in a HIP graph and replayed."""
+    if fused:
+        shapes = [(QuantType.Q4_K, 6144, 4096), (QuantType.Q4_K, 4096, 4096), (QuantType.Q4_K, 28672, 4096),
+                  (QuantType.Q6_K, 4096, 14336)]
+    else:
+        shapes = [(QuantType.Q4_K, 4096, 4096), (QuantType.Q4_K, 1024, 4096), (QuantType.Q4_K, 1024, 4096),
+                  (QuantType.Q4_K, 4096, 4096), (QuantType.Q4_K, 14336, 4096), (QuantType.Q4_K, 14336, 4096),
+                  (QuantType.Q6_K, 4096, 14336)]
     mats, total = [], 0
     seed = 0xDEC0DE
     for layer in range(layers):
@@ -214,23 +247,36 @@ def decode_workload(eng: Engine, batch: int, steps: int, warmup: int, layers: in
     launches = [(w.handle, C.c_void_p(x14 if k == 14336 else x4)) for (w, n, k) in mats]
     yp = C.c_void_p(y)
 
-    def enqueue(step):
+    def one_step():
         for h, xp in launches:
             rc = fn(h, xp, None, yp, batch, s)
             if rc:
                 check(rc, "decode")
 
+    g = None
+    if graph:
+        g = eng.hip.capture(eng.stream, one_step)
+
+        def enqueue(step):
+            eng.hip.graph_launch(g[0], eng.stream)
+    else:
+        def enqueue(step):
+            one_step()
+
     _, host_us, _ = eng.time_region(enqueue, warmup, 30.0 * len(launches))
     ms, _, host_bound = eng.time_region(enqueue, steps, host_us)
     per = ms / steps
+    if g:
+        eng.hip.graph_free(*g)
     for (w, _, _) in mats:
         eng.be.release(w)
     for p in (x4, x14, y):
         eng.hip.free(p)
     gbs = total / (per * 1e-3) / 1e9
-    log(f"decode B={batch}: {per:.3f} ms/step, {gbs:.0f} GB/s weights, {batch / (per * 1e-3):.0f} tok/s")
+    tag = ("fused" if fused else "unfused") + ("+graph" if graph else "")
+    log(f"decode B={batch} {tag}: {per:.3f} ms/step, {gbs:.0f} GB/s weights, {batch / (per * 1e-3):.0f} tok/s")
     return {
-        "workload": f"llama3-8b decode step B={batch}",
+        "workload": f"llama3-8b decode step B={batch} {tag}",
         "gemvs_per_step": len(launches),
         "batch": batch,
         "ms_per_step": round(per, 4),
@@ -400,7 +446,10 @@ def main():
         if "decode" in groups:
             dsteps = max(2, min(20, args.steps // 10))
             others.append(decode_workload(eng, 1, dsteps, 2))
+            others.append(decode_workload(eng, 1, dsteps, 2, fused=True))
+            others.append(decode_workload(eng, 1, dsteps, 2, fused=True, graph=True))
             others.append(decode_workload(eng, 16, max(2, dsteps // 4), 1))
+            others.append(decode_workload(eng, 16, max(2, dsteps // 4), 1, fused=True, graph=True))
 
     cpu = None if (args.quick or args.only) else cpu_baseline(args.cpu_seconds)
     per_ms = head["us_per_launch"] / 1e3

@@ -116,6 +116,11 @@ int j4q_upload_quantized_device(int quant_type, const void *device_blocks, uint6
                                 int64_t cols, j4q_buffer *out);
 /* Writes the matrix back as GGUF blocks (bit-exact inverse of the repack). */
 int j4q_export_quantized(j4q_buffer weights, void *blocks, uint64_t nbytes);
+/* One matrix whose rows are the rows of `parts` in order (same quant type and column count;
+ * engine-local, no SPI counterpart). Matrices that share their input, such as the q/k/v or
+ * gate/up projections of a decoder layer, then run as one GEMV launch: y holds the parts'
+ * outputs one after another. The parts stay valid and owned by the caller. */
+int j4q_concat_rows(const j4q_buffer *parts, int32_t count, j4q_buffer *out);
 /* ComputeBackend.upload for F32 data (spi/ComputeBackend.java:48). rank 1 or 2. */
 int j4q_upload_f32(const float *data, int32_t rank, const int64_t *dims, j4q_buffer *out);
 /* bf16 activations for the prefill GEMM (DType has no BF16, core/tensor/DType.java:19-21). */
@@ -164,6 +169,52 @@ int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *a
  * the bf16 variant ignores them. */
 int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, int8_t *xq_dev,
                           float *xs_dev, float *y_dev, void *stream);
+
+/* ---- GGUF files (the step before uploadQuantized; engine-local) ---------------------- */
+/* The reference receives quantized blobs from an external caller (spi/QuantizedOps.java:24)
+ * and knows the GGUF type ids (core/tensor/QuantType.java:3-13); this reader supplies them
+ * from a .gguf file (v2/v3). The file is mapped read-only and fully bounds-checked on open;
+ * malformed files fail with J4Q_EINVAL and a message naming the byte position. */
+typedef uint64_t j4q_gguf; /* 0 is never a valid handle */
+
+typedef struct j4q_gguf_info {
+    uint32_t version;
+    uint32_t reserved;
+    int64_t tensor_count;
+    int64_t metadata_count;
+    uint64_t alignment;    /* general.alignment, default 32 */
+    uint64_t data_offset;  /* file offset of the tensor data section */
+    uint64_t file_bytes;
+} j4q_gguf_info;
+
+typedef struct j4q_gguf_tensor {
+    char name[256];
+    int32_t type_id;       /* ggml type id (QuantType ids for the types the reference knows) */
+    int32_t n_dims;        /* 1..4 */
+    int64_t dims[4];       /* innermost first: a [rows, cols] matrix has dims {cols, rows, 1, 1} */
+    uint64_t offset;       /* absolute file offset of the data */
+    uint64_t nbytes;       /* 0 if the type's block geometry is unknown */
+} j4q_gguf_tensor;
+
+int j4q_gguf_open(const char *path, j4q_gguf *out);
+/* Unmaps the file. Closing 0 is a no-op. */
+int j4q_gguf_close(j4q_gguf f);
+int j4q_gguf_file_info(j4q_gguf f, j4q_gguf_info *out);
+int j4q_gguf_tensor_info(j4q_gguf f, int64_t index, j4q_gguf_tensor *out);
+int j4q_gguf_find_tensor(j4q_gguf f, const char *name, int64_t *index);
+/* Metadata entry `index`: key (truncated to cap - 1 bytes), GGUF value type (0 u8 .. 12 f64),
+ * array element type and count (string: count = byte length). Any out pointer may be NULL. */
+int j4q_gguf_meta_key(j4q_gguf f, int64_t index, char *key, int32_t cap, int32_t *type, int32_t *elem_type,
+                      uint64_t *count);
+/* Scalar metadata value, zero-extended into 8 bytes, and its GGUF type. */
+int j4q_gguf_meta_scalar(j4q_gguf f, const char *key, int32_t *type, void *value8);
+/* String metadata value (NUL-terminated, truncated to cap - 1 bytes) and its full length. */
+int j4q_gguf_meta_string(j4q_gguf f, const char *key, char *out, uint64_t cap, uint64_t *length);
+/* Copies tensor `index`'s blocks (exactly nbytes) to host memory. */
+int j4q_gguf_read_tensor(j4q_gguf f, int64_t index, void *dst, uint64_t nbytes);
+/* QuantizedOps.uploadQuantized of tensor `index` straight from the mapping (rows = product of
+ * dims[1..3], cols = dims[0]); the same type and size rules as j4q_upload_quantized. */
+int j4q_gguf_upload(j4q_gguf f, int64_t index, j4q_buffer *out);
 
 /* ---- seeded synthetic inputs (benchmark support; no reference counterpart) ------------- */
 

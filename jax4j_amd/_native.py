@@ -53,6 +53,29 @@ class BufferDesc(C.Structure):
     ]
 
 
+class GgufInfo(C.Structure):
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("reserved", C.c_uint32),
+        ("tensor_count", C.c_int64),
+        ("metadata_count", C.c_int64),
+        ("alignment", C.c_uint64),
+        ("data_offset", C.c_uint64),
+        ("file_bytes", C.c_uint64),
+    ]
+
+
+class GgufTensor(C.Structure):
+    _fields_ = [
+        ("name", C.c_char * 256),
+        ("type_id", C.c_int32),
+        ("n_dims", C.c_int32),
+        ("dims", C.c_int64 * 4),
+        ("offset", C.c_uint64),
+        ("nbytes", C.c_uint64),
+    ]
+
+
 _i32, _i64, _u64, _vp = C.c_int32, C.c_int64, C.c_uint64, C.c_void_p
 _buf = C.c_uint64
 _pbuf = C.POINTER(C.c_uint64)
@@ -72,6 +95,7 @@ SIGNATURES = {
     "j4q_upload_quantized": [C.c_int, _vp, _u64, _i64, _i64, _pbuf],
     "j4q_upload_quantized_device": [C.c_int, _vp, _u64, _i64, _i64, _pbuf],
     "j4q_export_quantized": [_buf, _vp, _u64],
+    "j4q_concat_rows": [_pbuf, _i32, _pbuf],
     "j4q_upload_f32": [_vp, _i32, C.POINTER(_i64), _pbuf],
     "j4q_upload_bf16": [_vp, _i32, C.POINTER(_i64), _pbuf],
     "j4q_download_f32": [_buf, _vp, _i64],
@@ -92,6 +116,16 @@ SIGNATURES = {
     "j4q_synth_bf16_host": [_u64, _i64, _vp],
     "j4q_synth_f32_device": [_u64, _i64, _vp, _vp],
     "j4q_synth_bf16_device": [_u64, _i64, _vp, _vp],
+    "j4q_gguf_open": [C.c_char_p, C.POINTER(_u64)],
+    "j4q_gguf_close": [_u64],
+    "j4q_gguf_file_info": [_u64, C.POINTER(GgufInfo)],
+    "j4q_gguf_tensor_info": [_u64, _i64, C.POINTER(GgufTensor)],
+    "j4q_gguf_find_tensor": [_u64, C.c_char_p, C.POINTER(_i64)],
+    "j4q_gguf_meta_key": [_u64, _i64, C.c_char_p, _i32, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_u64)],
+    "j4q_gguf_meta_scalar": [_u64, C.c_char_p, C.POINTER(_i32), _vp],
+    "j4q_gguf_meta_string": [_u64, C.c_char_p, C.c_char_p, _u64, C.POINTER(_u64)],
+    "j4q_gguf_read_tensor": [_u64, _i64, _vp, _u64],
+    "j4q_gguf_upload": [_u64, _i64, _pbuf],
     "j4q_spin": [C.c_uint32, _vp],
     "j4q_copy": [_vp, _vp, _u64, _vp],
 }

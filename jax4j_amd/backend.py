@@ -217,6 +217,18 @@ class Mi355xBackend:
         check(self._lib().j4q_quant_dequantize(weights.handle, C.byref(out)), "dequantize")
         return DeviceBuffer(out.value, tuple(weights.shape), DType.F32, weights.device)
 
+    def concat_rows(self, parts) -> DeviceBuffer:
+        """One quantized matrix holding the rows of ``parts`` in order (same type and cols):
+        matrices that share an input run as one GEMV (engine-local; no SPI counterpart)."""
+        parts = list(parts)
+        if not parts or any(p.quant_type is None for p in parts):
+            raise IllegalArgumentException("concat_rows needs quantized buffers")
+        arr = (C.c_uint64 * len(parts))(*[p.handle for p in parts])
+        out = C.c_uint64()
+        check(self._lib().j4q_concat_rows(arr, len(parts), C.byref(out)), "concat_rows")
+        rows = sum(p.shape[0] for p in parts)
+        return DeviceBuffer(out.value, (rows, parts[0].shape[1]), DType.F32, Device.rocm(self._device), parts[0].quant_type)
+
     def export_quantized(self, weights: DeviceBuffer) -> np.ndarray:
         nbytes = weights.quant_type.byte_size_for(weights.shape[0] * weights.shape[1])
         out = np.empty(nbytes, dtype=np.uint8)

@@ -62,6 +62,23 @@ int hip_fail(const char *op, hipError_t e) {
         if (e_ != hipSuccess) return hip_fail(op, e_); \
     } while (0)
 
+}  // namespace
+
+namespace j4q {
+// Error reporting for the GGUF reader (gguf.hip): same thread-local message as every entry point.
+int gguf_fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+}  // namespace j4q
+
+namespace {
+
 bool is_gfx950(const hipDeviceProp_t &p) { return strncmp(p.gcnArchName, "gfx950", 6) == 0; }
 
 // Requires g_mu held.
@@ -410,6 +427,61 @@ int j4q_export_quantized(j4q_buffer wh, void *blocks, uint64_t nbytes) {
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
     (void)hipFree(tmp);
     if (e != hipSuccess) return hip_fail("export", e);
+    return J4Q_OK;
+}
+
+int j4q_concat_rows(const j4q_buffer *parts, int32_t count, j4q_buffer *out) {
+    if (!parts || !out) return fail(J4Q_EINVAL, "concat_rows: NULL argument");
+    if (count < 1 || count > 64) return fail(J4Q_EINVAL, "concat_rows: count %d out of range [1, 64]", count);
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc;
+    std::vector<Buf *> ps((size_t)count);
+    int64_t rows = 0;
+    for (int i = 0; i < count; i++) {
+        if ((rc = get_buf(parts[i], J4Q_KIND_QUANT, "concat_rows", &ps[(size_t)i]))) return rc;
+        if (ps[(size_t)i]->qtype != ps[0]->qtype || ps[(size_t)i]->dims[1] != ps[0]->dims[1])
+            return fail(J4Q_EINVAL, "concat_rows: part %d is type %d with %lld columns; part 0 is type %d with %lld", i,
+                        ps[(size_t)i]->qtype, (long long)ps[(size_t)i]->dims[1], ps[0]->qtype, (long long)ps[0]->dims[1]);
+        rows += ps[(size_t)i]->dims[0];
+    }
+    const int qt = ps[0]->qtype;
+    const int64_t cols = ps[0]->dims[1];
+    if ((rc = check_sections(qt, rows, cols))) return rc;
+    if ((rc = ensure_ready())) return rc;
+    // every section of the split layout is row-major over rows, so each part's sections land
+    // at their row offset in the matching section of the result
+    const j4q::SplitLayout L = j4q::split_layout(qt, rows, cols);
+    void *dev = nullptr;
+    HIP_TRY("hipMalloc", hipMalloc(&dev, L.total));
+    hipError_t e = hipSuccess;
+    uint64_t off[4] = {0, 0, 0, 0};
+    for (int i = 0; i < count && e == hipSuccess; i++) {
+        const Buf &b = *ps[(size_t)i];
+        const j4q::SplitLayout P = j4q::split_layout(qt, b.dims[0], cols);
+        const uint64_t src_off[4] = {P.qs_off, P.qh_off, P.sc_off, P.d_off};
+        const uint64_t dst_off[4] = {L.qs_off, L.qh_off, L.sc_off, L.d_off};
+        const uint64_t len[4] = {P.qs_bytes, P.qh_bytes, P.sc_bytes, P.d_bytes};
+        for (int sct = 0; sct < 4 && e == hipSuccess; sct++) {
+            if (!len[sct]) continue;
+            e = hipMemcpyAsync((uint8_t *)dev + dst_off[sct] + off[sct], (const uint8_t *)b.dev + src_off[sct], len[sct],
+                               hipMemcpyDeviceToDevice, g_stream);
+            off[sct] += len[sct];
+        }
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail("concat_rows", e);
+    }
+    Buf nb;
+    nb.kind = J4Q_KIND_QUANT;
+    nb.qtype = qt;
+    nb.rank = 2;
+    nb.dims[0] = rows;
+    nb.dims[1] = cols;
+    nb.dev = dev;
+    nb.bytes = L.total;
+    *out = register_buf(nb);
     return J4Q_OK;
 }
 

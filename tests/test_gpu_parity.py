@@ -340,3 +340,28 @@ def test_concurrent_callers_get_serial_results(backend, uploaded):
     assert not errors
     for a, b in zip(results, serial):
         assert np.array_equal(bits(a), bits(b))
+
+
+@pytest.mark.parametrize("qt", [QuantType.Q4_K, QuantType.Q6_K, QuantType.Q8_0], ids=lambda q: q.name)
+@pytest.mark.parametrize("B", [1, 4])
+def test_concat_rows_fused_gemv(backend, qt, B):
+    """q/k/v-style fusion: one matrix over the parts' rows gives the parts' outputs bit for bit."""
+    cols = 512
+    shapes = [40, 24, 24]
+    note("concat", qt.name, shapes, cols, "B", B)
+    blobs = [S.quant_blocks(qt, 300 + i, r, cols) for i, r in enumerate(shapes)]
+    parts = [backend.upload_quantized(b, qt, (r, cols)) for b, r in zip(blobs, shapes)]
+    fused = backend.concat_rows(parts)
+    assert fused.shape == (sum(shapes), cols)
+    assert np.array_equal(backend.export_quantized(fused), np.concatenate(blobs))
+    xs = S.activations_f32(77 + B, B * cols).reshape(B, cols)
+    xb = backend.upload(xs if B > 1 else xs[0], shape=(B, cols) if B > 1 else None)
+    yf = backend.download(backend.quant_matvec(fused, xb)).reshape(B, -1)
+    off = 0
+    for p, r in zip(parts, shapes):
+        yp = backend.download(backend.quant_matvec(p, xb)).reshape(B, r)
+        assert np.array_equal(bits(yf[:, off:off + r]), bits(yp))
+        off += r
+    with pytest.raises(IllegalArgumentException):
+        other = backend.upload_quantized(S.quant_blocks(QuantType.Q4_0, 5, 8, cols), QuantType.Q4_0, (8, cols))
+        backend.concat_rows([parts[0], other])
