@@ -23,16 +23,34 @@ hipError_t launch_fmt(const QMat &m, const float *x, const float *add, float *y,
 
 int g_cus = 256;
 
+// Blocks per launch window of launch_mfma: 8 waves x items per wave x tile sets, 128
+// blocks (4096 columns) for every format.
+template <int FMT>
+constexpr int mfma_window() { return FMT == Q8_0 ? 8 * 8 * 2 : 8 * 4 * 4; }
+
 // Batched GEMV on the matrix cores (gemv_mfma.h) for up to 8 batch rows per launch:
-// persistent grid of one 8-wave workgroup per CU, K <= 4096 split into 8 wave slices of
-// 128 blocks / 8. Measured on MI355X (Q4_0 11008 x 4096): B = 4 11.8 us, B = 8 13.1 us,
-// against 22 us and 41 us for one vector-ALU pass per batch row; at B <= 2 the two are level.
+// persistent grid of one 8-wave workgroup per CU, each launch a window of up to 128 blocks
+// (4096 columns) split into 8 wave slices; a wider K runs as equal windows, each adding the
+// previous window's output. Measured on MI355X (Q4_0 11008 x 4096): B = 4 11.8 us, B = 8
+// 13.1 us, against 22 us and 41 us for one vector-ALU pass per batch row; at B <= 2 the
+// two are level.
 template <int FMT, int BB>
 hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
-    constexpr int IPW = FMT == Q8_0 ? 8 : 4;
+    constexpr int IPW = FMT == Q8_0 ? 8 : 4, S = FMT == Q8_0 ? 2 : 4, CAP = mfma_window<FMT>();
+    static_assert(CAP == 8 * IPW * S, "window = waves x items per wave x tile sets");
     const int tiles = (int)((m.rows + 15) / 16);
     const int grid = tiles < g_cus ? tiles : g_cus;
-    return gmf::launch_k<FMT, BB, 8, IPW, false, 2>(m, x, add, y, b, grid, s);
+    const int nb = (int)(m.cols / 32);
+    const int windows = (nb + CAP - 1) / CAP;
+    const int per = ((nb + windows - 1) / windows + S - 1) / S * S;  // equal windows, S-aligned
+    for (int kb0 = 0; kb0 < nb; kb0 += per) {
+        const int kbn = nb - kb0 < per ? nb - kb0 : per;
+        const bool last = kb0 + kbn >= nb;
+        const hipError_t e = gmf::launch_k<FMT, BB, 8, IPW, false, 2>(m, x, last ? add : nullptr, y, b, grid, s, kb0, kbn,
+                                                                        kb0 == 0 ? nullptr : y);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 template <int FMT>
@@ -40,11 +58,14 @@ hipError_t launch_mfma_fmt(const QMat &m, const float *x, const float *add, floa
     return b <= 4 ? launch_mfma<FMT, 4>(m, x, add, y, b, s) : launch_mfma<FMT, 8>(m, x, add, y, b, s);
 }
 
-bool mfma_supported(int id, const QMat &m) {
+bool mfma_supported(int id, const QMat &m, bool add_aliases_y) {
     const int64_t k = m.cols;
+    // several windows read add only in the last one, after y was rewritten: an add that
+    // overlaps y then keeps the single-pass vector-ALU kernel
+    if (add_aliases_y && k > 32 * mfma_window<Q4_0>()) return false;
     switch (id) {
-    case Q4_0: case Q4_K: case Q6_K: return k <= 4096 && k % 128 == 0;
-    case Q8_0: return k <= 4096 && k % 64 == 0;
+    case Q4_0: case Q4_K: case Q6_K: return k % 128 == 0;
+    case Q8_0: return k % 64 == 0;
     default: return false;
     }
 }
@@ -78,7 +99,8 @@ hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, 
                        hipStream_t s) {
     if (m.rows <= 0 || batch <= 0) return hipSuccess;
     if (m.cols > gemv_max_cols() || batch > 65535 || m.rows > (1 << 30)) return hipErrorInvalidValue;
-    if (batch < 3 || !mfma_supported(id, m)) return launch_valu(id, m, x, add, y, (int)batch, s);
+    const bool alias = add && add < y + batch * m.rows && y < add + batch * m.rows;
+    if (batch < 3 || !mfma_supported(id, m, alias)) return launch_valu(id, m, x, add, y, (int)batch, s);
     // batch rows in launches of up to 8 on the matrix cores; a remainder of 1 or 2 rows
     // takes the vector-ALU kernel, which is as fast there
     for (int64_t b0 = 0; b0 < batch;) {

@@ -154,22 +154,28 @@ struct Plan {
 };
 
 // grid: G_wg persistent workgroups of WAVES waves; workgroup w takes 16-row tiles w,
-// w + G_wg, ... Wave v owns blocks [v NBW, (v + 1) NBW) of K (NBW = IPW * S); blocks past
-// K / 32 load nothing and their x image is zero. Requires K % (32 S) == 0,
-// K <= WAVES * NBW * 32 and B <= BB. XREG keeps the wave's A operands and C inputs in
+// w + G_wg, ... The kernel covers the window of blocks [kb0, kb0 + kbn) of every row:
+// y = (W[:, window] x[window] + prev) + add, so a wider K runs as windows chained through
+// prev (each adding the previous window's y, read before that element is rewritten) and
+// the caller's add joins only in the last window.
+// Wave v owns window blocks [v NBW, (v + 1) NBW) (NBW = IPW * S); blocks past the window
+// load nothing and their x image is zero. Requires kb0 and kbn multiples of S,
+// kbn <= WAVES * NBW and B <= BB. XREG keeps the wave's A operands and C inputs in
 // registers for the whole kernel instead of re-reading them from LDS per tile.
 template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS>
 __global__ void __launch_bounds__(WAVES * 64)
-gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, float *__restrict__ y, int B) {
+gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const float *__restrict__ add, float *y,
+                 int B, int kb0, int kbn) {
     using F = Fmt<FMT>;
     constexpr int S = F::S, G = F::GROUPS, NBW = IPW * S;
     using P = Plan<BB, G, WAVES, NBW>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int K = (int)m.cols, N = (int)m.rows;
-    const int tiles = (N + 15) / 16, nb = K / 32;
+    const int tiles = (N + 15) / 16, nb = kb0 + kbn;  // blocks [kb0, nb) of every row
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
-    const int blkw = wave * NBW;  // first block of this wave's K slice
+    const int lw = wave * NBW;     // this wave's K slice: window blocks [lw, lw + NBW)
+    const int blkw = kb0 + lw;     // ... and its first block in the row
     const Rsrc rs = gemv::rsrc_of(m, FMT);
 
     // ---- 1. x image of this wave's slice, built before any weight load is issued --------
@@ -240,7 +246,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
         for (int i = 0; i < XPL; i++) {
             const int u = lane + 64 * i;
             const int bl = u / UNITS, rem = u - bl * UNITS, b = rem >> 2, gg = rem & 3;
-            const int blk = blkw + bl;
+            const int blk = lw + bl;  // x image index (window-relative)
             float s = 0.f;
 #pragma unroll
             for (int bb = 0; bb < BB; bb++) s = (b == bb) ? sx[bb] : s;
@@ -291,10 +297,10 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
     const int mrow = lane & 15;
     int abase, astride;
     if (mrow < BB) {
-        abase = P::kXa + ((blkw * 2 * BB + mrow) * 4 + g) * 16;
+        abase = P::kXa + ((lw * 2 * BB + mrow) * 4 + g) * 16;
         astride = 128 * BB;
     } else if (mrow >= 8 && mrow < 8 + BB) {
-        abase = P::kXa + ((blkw * 2 * BB + BB + mrow - 8) * 4 + g) * 16;
+        abase = P::kXa + ((lw * 2 * BB + BB + mrow - 8) * 4 + g) * 16;
         astride = 128 * BB;
     } else {
         abase = P::kZero + g * 16;
@@ -303,7 +309,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
     constexpr int JB = BB < 4 ? BB : 4;  // C rows per lane that carry a batch row
     const int hb = 4 * (g & 1);          // first batch row of this lane's C rows
     const bool hi_lane = g < 2 && hb < BB;
-    const int cbase = hi_lane ? P::kCin + (blkw * G * BB + hb) * 4 : P::kZero;
+    const int cbase = hi_lane ? P::kCin + (lw * G * BB + hb) * 4 : P::kZero;
     const int cstride = hi_lane ? G * BB * 4 : 0;
     auto a_op = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + bl * astride); };
     auto c_in = [&](int bl, int k) { return reinterpret_cast<const float *>(lds + cbase + bl * cstride)[k]; };
@@ -320,14 +326,16 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
     }
 
     // ---- 2. weight loads of the first two tiles -----------------------------------------
-    // The reducing threads (b, nn) = (tid / 16, tid % 16), tid < 16 BB, also fetch add[b][row]
-    // with the tile's weights, so waiting for it never drains the loads issued later.
+    // The reducing threads (b, nn) = (tid / 16, tid % 16), tid < 16 BB, also fetch prev[b][row]
+    // and add[b][row] with the tile's weights, so waiting for them never drains the loads
+    // issued later.
     const __amdgpu_buffer_rsrc_t addr = make_rsrc(add ? (const void *)add : (const void *)y, add ? (uint64_t)B * N * 4u : 0);
+    const __amdgpu_buffer_rsrc_t prevr = make_rsrc(prev ? (const void *)prev : (const void *)y, prev ? (uint64_t)B * N * 4u : 0);
     const int rb = (int)threadIdx.x >> 4, rn = (int)threadIdx.x & 15;
     // Q4_0 scales: one load per tile, lane group g fetching item g's four (16 rows x 32 B
     // instead of 16 rows x 8 B per item); process() broadcasts them across the groups.
     static_assert(FMT != Q4_0 || IPW <= 4, "Q4_0 tile scales cover four items");
-    auto load_tile = [&](F (&it)[IPW], float &av, int tile) {
+    auto load_tile = [&](F (&it)[IPW], f32x2 &av, int tile) {
         const bool live = tile < tiles;
         const int r = tile * 16 + n;
         const uint32_t row = (uint32_t)(r < N ? r : N - 1);
@@ -340,10 +348,12 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
         }
         const int ar = tile * 16 + rn;
         const bool aok = live && (int)threadIdx.x < 16 * BB && rb < B && ar < N;
-        av = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(addr, aok ? (uint32_t)(rb * N + ar) * 4u : kOob, 0, 0));
+        const uint32_t ao = aok ? (uint32_t)(rb * N + ar) * 4u : kOob;
+        av.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prevr, ao, 0, 0));
+        av.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(addr, ao, 0, 0));
     };
     F ta[IPW], tb[TS == 2 ? IPW : 1];
-    float aa, ab;
+    f32x2 aa, ab;
     const int t0 = (int)blockIdx.x, tstep = (int)gridDim.x;
     __builtin_amdgcn_sched_barrier(0);
     load_tile(ta, aa, t0);
@@ -365,7 +375,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
 
     // ---- 3. per tile: transpose, unpack, MFMA, block scale; partials through LDS ----------
     float *part = reinterpret_cast<float *>(lds + P::kPart);
-    auto process = [&](const F (&it)[IPW], float av, int tile, int parity) {
+    auto process = [&](const F (&it)[IPW], f32x2 av, int tile, int parity) {
         float acc[JB], corr[JB];
 #pragma unroll
         for (int j = 0; j < JB; j++) acc[j] = corr[j] = 0.f;
@@ -497,7 +507,9 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
             float s = 0.f;
             for (int w = 0; w < WAVES; w++) s += pp[(w * BB + rb) * 16 + rn];
             const int r = tile * 16 + rn;
-            if (rb < B && r < N) y[(int64_t)rb * N + r] = add ? s + av : s;
+            // the previous window's sum first, then add on its own: fl(fl(W.x) + add)
+            if (prev) s += av.x;
+            if (rb < B && r < N) y[(int64_t)rb * N + r] = add ? s + av.y : s;
         }
     };
 
@@ -524,10 +536,12 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ 
 }
 
 template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS = 2>
-hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, int B, int grid, hipStream_t s) {
+hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, int B, int grid, hipStream_t s,
+                    int kb0 = 0, int kbn = -1, const float *prev = nullptr) {
+    if (kbn < 0) kbn = (int)(m.cols / 32);
     constexpr int NBW = IPW * Fmt<FMT>::S;
     constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW>::kBytes;
-    gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<grid, WAVES * 64, lds, s>>>(m, x, add, y, B);
+    gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<grid, WAVES * 64, lds, s>>>(m, x, prev, add, y, B, kb0, kbn);
     return hipGetLastError();
 }
 

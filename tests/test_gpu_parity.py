@@ -234,6 +234,65 @@ def test_gemv_batched_matches_oracle(backend, uploaded, qt, rows, cols, B):
         backend.release(h)
 
 
+# K above one 4096-column launch window: the batched kernel runs equal windows, each adding
+# the previous window's y, and the caller's add joins only in the last one (11008 = three
+# windows of 116, 116 and 112 blocks; 14336 = four of 112).
+WIDE_CASES = [
+    (QuantType.Q4_0, 700, 11008), (QuantType.Q8_0, 300, 8192),
+    (QuantType.Q4_K, 300, 12288), (QuantType.Q6_K, 512, 14336),
+]
+
+
+@pytest.mark.parametrize("qt,rows,cols", WIDE_CASES, ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [3, 8, 16])
+def test_gemv_batched_wide_k(backend, uploaded, qt, rows, cols, B):
+    note("batched wide", qt.name, rows, cols, "B", B)
+    blob, w = uploaded(qt, rows, cols)
+    xs = S.activations_f32(rows + 11 * B, B * cols).reshape(B, cols)
+    add = S.activations_f32(rows + 13, B * rows).reshape(B, rows)
+    xb = backend.upload(xs, shape=(B, cols))
+    ab = backend.upload(add, shape=(B, rows))
+    y = backend.quant_matvec(w, xb)
+    ya = backend.quant_matvec_add(w, xb, ab)
+    got = backend.download(y).reshape(B, rows)
+    gota = backend.download(ya).reshape(B, rows)
+    # The matrix-core sums of one block round in one direction (a bias of a fraction of an
+    # fp32 ulp of the block's largest product, times its scale d > 0), so the error grows
+    # with the number of blocks: 1.0e-5 measured for Q4_0 at K = 11008. The bound stays 25x
+    # inside the decode tolerance TOL.
+    for b in range(B):
+        y64 = oracle.matvec_f64(qt.id, blob, rows, cols, xs[b])
+        assert rel_err(got[b], y64) <= 4e-5, f"row {b}"
+    assert np.array_equal(bits(gota), bits(got + add))
+    for h in (xb, ab, y, ya):
+        backend.release(h)
+
+
+@pytest.mark.parametrize("cols", [4096, 11008])
+def test_gemv_batched_add_in_place(backend, uploaded, cols):
+    """quantMatvecAdd with y on the add buffer itself (a residual updated in place)."""
+    qt, rows, B = QuantType.Q4_0, 1000, 8
+    note("batched in-place add", qt.name, rows, cols, "B", B)
+    blob, w = uploaded(qt, rows, cols)
+    xs = S.activations_f32(rows + 3, B * cols).reshape(B, cols)
+    add = S.activations_f32(rows + 4, B * rows).reshape(B, rows)
+    xb = backend.upload(xs, shape=(B, cols))
+    ab = backend.upload(add, shape=(B, rows))
+    ref = backend.download(backend.quant_matvec_add(w, xb, ab)).reshape(B, rows)
+    res = backend.upload(add, shape=(B, rows))
+    rp = backend.buffer_desc(res).device_ptr
+    backend.quant_matvec_into(w, backend.buffer_desc(xb).device_ptr, rp, rp, B)
+    backend.sync()
+    got = backend.download(res).reshape(B, rows)
+    if cols <= 4096:  # one window: the same kernel as the out-of-place call
+        assert np.array_equal(bits(got), bits(ref))
+    for b in range(B):
+        y64 = oracle.matvec_f64(qt.id, blob, rows, cols, xs[b]) + add[b].astype(np.float64)
+        assert rel_err(got[b], y64) <= 4e-5, f"row {b}"
+    for h in (xb, ab, res):
+        backend.release(h)
+
+
 @pytest.mark.parametrize("qt", [QuantType.Q4_0, QuantType.Q8_0, QuantType.Q4_K, QuantType.Q6_K], ids=lambda q: q.name)
 def test_gemv_batched_one_hot_and_range(backend, uploaded, qt):
     rows, cols = (300, 2304) if qt in (QuantType.Q4_K, QuantType.Q6_K) else (300, 1024)
