@@ -448,8 +448,8 @@ int j4q_concat_rows(const j4q_buffer *parts, int32_t count, j4q_buffer *out) {
     const int64_t cols = ps[0]->dims[1];
     if ((rc = check_sections(qt, rows, cols))) return rc;
     if ((rc = ensure_ready())) return rc;
-    // every section of the split layout is row-major over rows, so each part's sections land
-    // at their row offset in the matching section of the result
+    // every row-major section of the split layout lands at the part's row offset in the
+    // matching section of the result; Q8_0's block-major scale copy is rebuilt afterwards
     const j4q::SplitLayout L = j4q::split_layout(qt, rows, cols);
     void *dev = nullptr;
     HIP_TRY("hipMalloc", hipMalloc(&dev, L.total));
@@ -460,7 +460,7 @@ int j4q_concat_rows(const j4q_buffer *parts, int32_t count, j4q_buffer *out) {
         const j4q::SplitLayout P = j4q::split_layout(qt, b.dims[0], cols);
         const uint64_t src_off[4] = {P.qs_off, P.qh_off, P.sc_off, P.d_off};
         const uint64_t dst_off[4] = {L.qs_off, L.qh_off, L.sc_off, L.d_off};
-        const uint64_t len[4] = {P.qs_bytes, P.qh_bytes, P.sc_bytes, P.d_bytes};
+        const uint64_t len[4] = {P.qs_bytes, P.qh_bytes, P.sc_bytes, qt == j4q::Q8_0 ? 0 : P.d_bytes};
         for (int sct = 0; sct < 4 && e == hipSuccess; sct++) {
             if (!len[sct]) continue;
             e = hipMemcpyAsync((uint8_t *)dev + dst_off[sct] + off[sct], (const uint8_t *)b.dev + src_off[sct], len[sct],
@@ -468,6 +468,7 @@ int j4q_concat_rows(const j4q_buffer *parts, int32_t count, j4q_buffer *out) {
             off[sct] += len[sct];
         }
     }
+    if (e == hipSuccess && qt == j4q::Q8_0) e = j4q::launch_q8_scales_t(j4q::qmat_view((const uint8_t *)dev, qt, rows, cols), g_stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) {
         (void)hipFree(dev);

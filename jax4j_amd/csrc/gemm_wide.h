@@ -1,0 +1,267 @@
+// Prefill GEMM, bf16 variant for M >= 512: Y[M, N] = X[M, K] . bf16(W)[N, K]^T over Q8_0
+// weights, fp32 output.
+//
+// Tile 128 x 64 NJ per workgroup of 8 waves (NJ = 1 or 2), two waves per SIMD. K advances
+// in stages of 64 (two Q8_0 blocks); wave w owns columns [16 NJ (w % 4), 16 NJ (w % 4 + 1))
+// of the tile and block w / 4 of every stage, for all 128 rows: 8 x NJ
+// v_mfma_f32_16x16x32_bf16 accumulators. The two waves that share columns (one per block of
+// a stage) add their partial tiles through LDS at the end, in a fixed order.
+//
+// What bounds it is the rate at which a CU's vector memory path accepts cache lines (about
+// one 128-byte line per 4 clocks, measured): every load instruction here touches only whole
+// lines, 8 per instruction.
+//  - X (bf16, rows 8 KB apart for K = 4096): 128 rows x 128 bytes per stage, 8 rows per
+//    load instruction, stored with 128-bit writes into three LDS stage buffers of 128-byte
+//    rows whose 16-byte chunks are XOR-swizzled by the row (chunk c of row r at
+//    c ^ ((r / 2) % 8)): the LDS serves 16 lanes of a 128-bit access per cycle from 64
+//    banks, and the 16 rows of an MFMA operand read then fall on distinct banks.
+//  - W int8: 128 bytes (four blocks, two stages) of each of the tile's rows per load, 8 rows
+//    per instruction, into an LDS buffer with rows padded to 144 bytes; each wave reads its
+//    8 bytes per lane from there and dequantizes them in registers to bf16(d * q) (d * q is
+//    exact in fp32, the conversion rounds to nearest even).
+//  - W scales from the block-major copy of the Q8_0 split layout: the 16 rows of an operand
+//    tile read one contiguous 32-byte run per block.
+//  - MFMA lane group g = lane / 16 supplies k = 8 g + 0..7 of its block, for A (X) and B (W)
+//    alike.
+// Pipeline, one barrier per stage: global loads run R stages ahead in a ring of register
+// sets; X of stage i + 2 (and W of its stage pair) is stored into LDS while the MFMA
+// operands of stage i + 1 are read and the MFMAs of stage i run on operands read one
+// iteration earlier, so LDS traffic and matrix work overlap. A buffer is rewritten only
+// after every wave passed the barrier that follows its last read. The ring has no branch:
+// the stages past the end (at most R - 1) load zeros and add exact zeros, which keeps the
+// compiler's memory-counter waits exact.
+#pragma once
+
+#include "j4q_common.h"
+
+namespace j4q {
+namespace gw {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr uint32_t kOob = 0x80000000u;
+constexpr int BM = 128;
+constexpr int kStageBytes = BM * 128;  // X: 64 bf16 of k per row
+constexpr int kWRow = 144;             // W LDS row: 128 bytes (two stages) + 16 bytes of padding
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint64_t bytes) {
+    const uint32_t n = bytes > 0x7fffffffull ? 0x7fffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)n, 0x00020000);
+}
+
+// bf16(d * q) of the 8 int8 in q, packed as an MFMA operand.
+__device__ __forceinline__ bf16x8 dequant8(u32x2 q, float d) {
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t v = q[j];
+        const float f0 = d * (float)(int8_t)(v & 0xFFu), f1 = d * (float)(int8_t)((v >> 8) & 0xFFu);
+        const float f2 = d * (float)(int8_t)((v >> 16) & 0xFFu), f3 = d * (float)(int8_t)(v >> 24);
+        o[2 * j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{f0, f1}), bf16x2));
+        o[2 * j + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{f2, f3}), bf16x2));
+    }
+    return __builtin_bit_cast(bf16x8, o);
+}
+
+// grid = ceil(M / 128) * ceil(N / (64 NJ)) workgroups of 512 threads. Requires K % 32 == 0,
+// M * K * 2 < 2^31, N * K < 2^31 and the block-major scale copy in w.d.
+template <int NJ, int R>
+__global__ void __launch_bounds__(512)
+gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M) {
+    static_assert(R % 2 == 0 && R >= 4, "the ring unrolls by an even R of at least 4");
+    constexpr int BN = 64 * NJ;
+    constexpr int kWBuf = BN * kWRow;
+    constexpr int kXRegion = 3 * kStageBytes;
+    constexpr int kRedBytes = 4 * 8 * NJ * 4 * 64 * 4;  // partial tiles of the 4 second-block waves
+    constexpr int kLds = kXRegion + 2 * kWBuf > kRedBytes ? kXRegion + 2 * kWBuf : kRedBytes;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (K + 63) / 64;
+    const int mt = (M + BM - 1) / BM;
+    // Workgroup b runs on XCD b % 8; tile order is m fastest and each XCD takes a contiguous
+    // range of it, so the m tiles of a group of n tiles (the same W rows) share an L2.
+    const int total = (int)gridDim.x;
+    int tile = (int)blockIdx.x;
+    if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nw = wave & 3, kh = wave >> 2;  // column group, block of the stage
+    const int m16 = lane & 15, g = lane >> 4;
+
+    // X: thread t stages chunks q = t + 512 j (row q / 8, 16-byte chunk q % 8) of a stage.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint64_t)M * (uint64_t)K * 2u);
+    uint32_t xoff[2];
+    int xk[2], xlds[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int q = tid + 512 * j, row = q >> 3, c = q & 7, gm = m0 + row;
+        xoff[j] = gm < M ? (uint32_t)gm * (uint32_t)K * 2u + (uint32_t)c * 16u : kOob;
+        xk[j] = c * 8;
+        xlds[j] = row * 128 + ((c ^ ((row >> 1) & 7)) << 4);
+    }
+    // W bytes: thread t stages chunks q = t + 512 j (tile row q / 8, 16-byte chunk q % 8) of
+    // the 128 bytes a stage pair covers.
+    const __amdgpu_buffer_rsrc_t wq = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
+    uint32_t woff[NJ];
+    int wk[NJ], wlds[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int q = tid + 512 * j, row = q >> 3, c = q & 7, n = n0 + row;
+        woff[j] = n < N ? (uint32_t)n * (uint32_t)K + (uint32_t)c * 16u : kOob;
+        wk[j] = c * 16;
+        wlds[j] = row * kWRow + c * 16;
+    }
+    // W scales: lane (row 16 j + lane % 16 of the wave's columns) reads the scale of block
+    // kh of the stage from the block-major copy.
+    const __amdgpu_buffer_rsrc_t wd = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
+    uint32_t doff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int n = n0 + 16 * NJ * nw + 16 * j + m16;
+        doff[j] = n < N ? (uint32_t)n * 2u : kOob;
+    }
+
+    struct Set {
+        u32x4 x[2];
+        u32x4 q[NJ];  // loaded with even stages only: the stage pair's W bytes
+        uint32_t d[NJ];
+    };
+    Set set[R];
+    // Stage i covers k [64 i, 64 i + 64); stages at or past ns (and blocks past the row)
+    // load nothing.
+    auto load = [&](int i, Set &S_, bool pair) {
+        const bool live = i < ns;
+        const int k0 = i * 64;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const bool ok = live && k0 + xk[j] < K;
+            S_.x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff[j] : kOob, (uint32_t)k0 * 2u, 0));
+        }
+        if (pair) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const bool ok = live && k0 + wk[j] < K;
+                S_.q[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wq, ok ? woff[j] : kOob, (uint32_t)k0, 0));
+            }
+        }
+        const int kb = 2 * i + kh;  // this wave's block (wave-uniform)
+        const bool bok = live && kb < nblk;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            S_.d[j] = __builtin_amdgcn_raw_buffer_load_b16(wd, doff[j], bok ? (uint32_t)kb * (uint32_t)N * 2u : kOob, 0);
+    };
+
+    f32x4 acc[8][NJ];
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 bfr[2][NJ];  // B operands of a stage, double-buffered
+
+    uint8_t *const xbase = lds;
+    uint8_t *const wbase = lds + kXRegion;
+    auto store_x = [&](const Set &S_, int buf) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) *reinterpret_cast<u32x4 *>(&xbase[buf * kStageBytes + xlds[j]]) = S_.x[j];
+    };
+    auto store_w = [&](const Set &S_, int wbuf) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) *reinterpret_cast<u32x4 *>(&wbase[wbuf * kWBuf + wlds[j]]) = S_.q[j];
+    };
+    // B operand bytes of stage i for column tile j: row 16 NJ nw + 16 j + lane % 16, bytes
+    // 32 (2 (i % 2) + kh) + 8 g of the stage pair's 128.
+    const int wrd = (16 * NJ * nw + m16) * kWRow + 32 * kh + 8 * g;
+    auto read_w = [&](int wbuf, int odd, u32x2 (&wb)[NJ]) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) wb[j] = *reinterpret_cast<const u32x2 *>(&wbase[wbuf * kWBuf + wrd + 16 * j * kWRow + 64 * odd]);
+    };
+    // A operand of row tile t: row 16 t + lane % 16, chunk 4 kh + g (the swizzle term
+    // (row / 2) % 8 does not depend on t).
+    const int aoff = m16 * 128 + (((4 * kh + g) ^ ((m16 >> 1) & 7)) << 4);
+    auto read_a = [&](int buf, bf16x8 (&a)[8]) {
+#pragma unroll
+        for (int t = 0; t < 8; t++) a[t] = *reinterpret_cast<const bf16x8 *>(&xbase[buf * kStageBytes + t * 16 * 128 + aoff]);
+    };
+
+    // Prologue: stages 0 .. R-1 in flight; X of stages 0 and 1 and W of pair 0 in LDS; the
+    // operands of stage 0 read and dequantized.
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        load(r, set[r], (r & 1) == 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    bf16x8 a[2][8];
+    u32x2 wb[NJ];
+    store_x(set[0], 0);
+    store_x(set[1], 1);
+    store_w(set[0], 0);
+    __syncthreads();
+    read_a(0, a[0]);
+    read_w(0, 0, wb);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) bfr[0][j] = dequant8(wb[j], half_bits_to_float(set[0].d[j]));
+    // Iteration i (set i % R, X buffer i % 3, W buffer (i / 2) % 2): the barrier publishes X
+    // of stage i + 1 (and W of its pair) and frees the buffers of stage i - 1; then the loads
+    // of stage i + R, the operand reads of stage i + 1, the stores of stage i + 2, the
+    // dequantization of stage i + 1 and the MFMAs of stage i.
+    int b0 = 0;  // i % 3
+    for (int i0 = 0; i0 < ns; i0 += R) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            // i0 is a multiple of the even R, so i % 2 == r % 2
+            const int i = i0 + r;
+            const int b1 = b0 == 2 ? 0 : b0 + 1, b2 = b1 == 2 ? 0 : b1 + 1;
+            __syncthreads();
+            load(i + R, set[r], (r & 1) == 0);
+            __builtin_amdgcn_sched_barrier(0);
+            // the LDS traffic goes first: the wait before the next barrier then finds it done
+            read_a(b1, a[(r + 1) & 1]);
+            read_w(((i + 1) >> 1) & 1, (r + 1) & 1, wb);
+            store_x(set[(r + 2) % R], b2);
+            if ((r & 1) == 0) store_w(set[(r + 2) % R], ((i + 2) >> 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) bfr[(r + 1) & 1][j] = dequant8(wb[j], half_bits_to_float(set[(r + 1) % R].d[j]));
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r & 1][t], bfr[r & 1][j], acc[t][j], 0, 0, 0);
+            b0 = b1;
+        }
+    }
+
+    // ---- epilogue: the second-block waves hand their partial tiles to the first-block
+    // waves, which add them (first + second) and store. Result element v of tile (t, j) is
+    // row 16 t + 4 g + v, column 16 j + lane % 16 of the wave's columns.
+    float *red = reinterpret_cast<float *>(lds);
+    __syncthreads();  // every wave is past its last read of the stage buffers
+    if (kh == 1) {
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) red[(((nw * 8 + t) * NJ + j) * 4 + v) * 64 + lane] = acc[t][j][v];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int row = m0 + 16 * t + 4 * g + v, col = n0 + 16 * NJ * nw + 16 * j + m16;
+                const float s = acc[t][j][v] + red[(((nw * 8 + t) * NJ + j) * 4 + v) * 64 + lane];
+                if (row < M && col < N) y[(int64_t)row * N + col] = s;
+            }
+}
+
+}  // namespace gw
+}  // namespace j4q

@@ -3,13 +3,16 @@
 // Engine-resident weight layout ("split layout"). uploadQuantized copies the caller's
 // GGUF blob to HBM and repacks it once into per-row arrays whose 16-byte chunks each
 // hold 32 consecutive elements, so the GEMV streams every row with aligned 128-bit
-// loads. The repack is a bijection on bits: bytes per matrix are exactly the GGUF
-// byte count, and gather/export reproduce the GGUF values bit for bit.
+// loads. The repack is a bijection on bits: gather/export reproduce the GGUF values bit
+// for bit, and bytes per matrix are the GGUF byte count (plus, for Q8_0 only, a second
+// copy of the scales for the prefill GEMM).
 //
 //   Q4_0 : qs  [N][K/2]    chunk j byte i: lo nibble = elem 32j+i, hi = elem 32j+16+i
 //          sc  [N][K/32]   fp16 d
 //   Q8_0 : qs  [N][K]      int8, natural order
 //          sc  [N][K/32]   fp16 d
+//          d   [K/32][N]   the same fp16 d block-major: the 16 rows of a GEMM operand
+//                          tile read one cache line per block
 //   Q4_K : qs  [N][K/2]    chunk = one 32-element sub-block, nibble order as Q4_0
 //          sc  [N][K/256]  16 B: d fp16 | dmin fp16 | D0 | D1 | D2 where
 //                          D0 nibble j = scale_j & 15, D1 nibble j = min_j & 15,
@@ -72,7 +75,7 @@ __host__ __device__ inline SplitLayout split_layout(int id, int64_t rows, int64_
     const uint64_t n = (uint64_t)rows, k = (uint64_t)cols;
     switch (id) {
     case Q4_0: L.qs_bytes = n * k / 2; L.sc_bytes = n * (k / 32) * 2; break;
-    case Q8_0: L.qs_bytes = n * k; L.sc_bytes = n * (k / 32) * 2; break;
+    case Q8_0: L.qs_bytes = n * k; L.sc_bytes = n * (k / 32) * 2; L.d_bytes = L.sc_bytes; break;
     case Q4_K: L.qs_bytes = n * k / 2; L.sc_bytes = n * (k / 256) * 16; break;
     case Q6_K:
         L.qs_bytes = n * k / 2;
@@ -115,6 +118,8 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
 namespace j4q {
 hipError_t launch_repack(int id, const uint8_t *gguf, uint8_t *split, int64_t rows, int64_t cols,
                          hipStream_t s);
+// Q8_0: rewrite the block-major scale copy (d) from the row-major scales (sc).
+hipError_t launch_q8_scales_t(const QMat &m, hipStream_t s);
 hipError_t launch_export(int id, const uint8_t *split, uint8_t *gguf, int64_t rows, int64_t cols,
                          hipStream_t s);
 hipError_t launch_dequant_rows(int id, const QMat &m, int64_t row0, int64_t nrows, float *out,

@@ -68,6 +68,7 @@ repack_kernel(int id, const uint8_t *__restrict__ src, uint8_t *__restrict__ bas
         uint8_t *dst = qs + row * cols + j * 32;
         for (int i = 0; i < 32; i++) dst[i] = b[2 + i];
         st16(sc + (row * bpr + j) * 2, ld16(b));
+        st16(const_cast<uint8_t *>(m.d) + (j * rows + row) * 2, ld16(b));
         break;
     }
     case Q2_0: {
@@ -314,6 +315,15 @@ __global__ void __launch_bounds__(kThreads) synth_bf16_kernel(uint64_t seed, int
     if (i < n) out[i] = j4q_synth::f32_to_bf16(j4q_synth::synth_x(seed, (uint64_t)i));
 }
 
+// One thread per (row, block): d[block][row] = sc[row][block].
+__global__ void __launch_bounds__(kThreads) q8_scales_t_kernel(QMat m) {
+    const int64_t bpr = m.cols / 32, n = m.rows * bpr;
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int64_t row = i / bpr, j = i % bpr;
+    st16(const_cast<uint8_t *>(m.d) + (j * m.rows + row) * 2, ld16(m.sc + i * 2));
+}
+
 inline unsigned grid_for(int64_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
 
 }  // namespace
@@ -324,6 +334,13 @@ hipError_t launch_repack(int id, const uint8_t *gguf, uint8_t *split, int64_t ro
     const int64_t n = rows * (cols / g.block_elements);
     if (n == 0) return hipSuccess;
     repack_kernel<<<grid_for(n), kThreads, 0, s>>>(id, gguf, split, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_scales_t(const QMat &m, hipStream_t s) {
+    const int64_t n = m.rows * (m.cols / 32);
+    if (n == 0) return hipSuccess;
+    q8_scales_t_kernel<<<grid_for(n), kThreads, 0, s>>>(m);
     return hipGetLastError();
 }
 

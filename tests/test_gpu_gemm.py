@@ -94,6 +94,28 @@ def test_gemm_bf16_matches_reference(backend, m, n, k):
         backend.release(h)
 
 
+# M >= 512 runs the wide-tile kernel: 128 x 64 tiles while 128 x 128 ones would be fewer
+# than 256 (one stage; a half stage at the end; tails in M and N), 128 x 128 from 256 tiles.
+WIDE_SHAPES = [(512, 128, 64), (600, 200, 96), (640, 520, 2048), (2048, 2048, 128)]
+
+
+@pytest.mark.parametrize("m,n,k", WIDE_SHAPES)
+def test_gemm_bf16_wide_tiles(backend, m, n, k):
+    note("gemm bf16 wide", m, n, k)
+    w_blob, xb, w, x = upload_case(backend, m, n, k, 3000 + m + n + k)
+    y = backend.quant_matmul(w, x, "bf16")
+    got = backend.download(y).reshape(m, n)
+    assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k, bf16_weights=True)) <= TOL_ACCUM
+    assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k)) <= TOL_BF16X
+    # repeated calls agree bit for bit
+    for _ in range(3):
+        y2 = backend.quant_matmul(w, x, "bf16")
+        assert np.array_equal(bits(backend.download(y2).reshape(m, n)), bits(got))
+        backend.release(y2)
+    for h in (w, x, y):
+        backend.release(h)
+
+
 def test_gemm_full_size_rows_and_variants_agree(backend):
     """configs[3] at full size (M=512, N=K=4096): sampled rows against the oracle, and the
     two variants against each other."""
