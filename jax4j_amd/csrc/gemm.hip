@@ -408,12 +408,12 @@ hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64
     if (m <= 0 || w.rows <= 0) return hipSuccess;
     if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols * 2 > 0x7fffffffull) return hipErrorInvalidValue;
     if (m >= 512 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
-        // 128 x 128 tiles (gemm_wide.h) when they fill the GPU, else 128 x 64
-        const int64_t mt = (m + gw::BM - 1) / gw::BM;
-        const int64_t t2 = mt * ((w.rows + 127) / 128), t1 = mt * ((w.rows + 63) / 64);
-        if (t1 > 0x7fffffff) return hipErrorInvalidValue;
-        if (t2 >= 256) gw::gemm_bf16_wide<2, 4><<<(unsigned)t2, 512, 0, s>>>(w, x, y, (int)m);
-        else gw::gemm_bf16_wide<1, 4><<<(unsigned)t1, 512, 0, s>>>(w, x, y, (int)m);
+        // gemm_wide.h: 128 x 128 tiles when they fill the GPU, else 128 x 64 (measured on
+        // MI355X, M = 512: 38.3 us against 39.7 us for 64 x 128 tiles)
+        const int64_t mt = (m + 127) / 128, t128 = mt * ((w.rows + 127) / 128), t64 = mt * ((w.rows + 63) / 64);
+        if (t64 > 0x7fffffff) return hipErrorInvalidValue;
+        if (t128 >= 256) gw::gemm_bf16_wide<128, 2, 4><<<(unsigned)t128, 512, 0, s>>>(w, x, y, (int)m);
+        else gw::gemm_bf16_wide<128, 1, 4><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
         return hipGetLastError();
     }
     if (m <= 64) return launch_gemm<kVarBf16, 64, 64, 4, 3, 2>(w, x, nullptr, y, m, s);

@@ -1,16 +1,18 @@
 // Prefill GEMM, bf16 variant for M >= 512: Y[M, N] = X[M, K] . bf16(W)[N, K]^T over Q8_0
 // weights, fp32 output.
 //
-// Tile 128 x 64 NJ per workgroup of 8 waves (NJ = 1 or 2), two waves per SIMD. K advances
-// in stages of 64 (two Q8_0 blocks); wave w owns columns [16 NJ (w % 4), 16 NJ (w % 4 + 1))
-// of the tile and block w / 4 of every stage, for all 128 rows: 8 x NJ
-// v_mfma_f32_16x16x32_bf16 accumulators. The two waves that share columns (one per block of
-// a stage) add their partial tiles through LDS at the end, in a fixed order.
+// Tile BM x 64 NJ (BM = 64 or 128, NJ = 1 or 2) per workgroup of 8 waves, two waves per
+// SIMD. K advances in stages of 64 (two Q8_0 blocks); wave w owns columns
+// [16 NJ (w % 4), 16 NJ (w % 4 + 1)) of the tile and block w / 4 of every stage, for all BM
+// rows: BM / 16 x NJ v_mfma_f32_16x16x32_bf16 accumulators. Each operand read from LDS
+// feeds NJ MFMAs, so NJ = 2 halves the LDS reads per flop. The two waves that share
+// columns (one per block of a stage) add their partial tiles through LDS at the end, in a
+// fixed order.
 //
 // What bounds it is the rate at which a CU's vector memory path accepts cache lines (about
 // one 128-byte line per 4 clocks, measured): every load instruction here touches only whole
 // lines, 8 per instruction.
-//  - X (bf16, rows 8 KB apart for K = 4096): 128 rows x 128 bytes per stage, 8 rows per
+//  - X (bf16, rows 8 KB apart for K = 4096): BM rows x 128 bytes per stage, 8 rows per
 //    load instruction, stored with 128-bit writes into three LDS stage buffers of 128-byte
 //    rows whose 16-byte chunks are XOR-swizzled by the row (chunk c of row r at
 //    c ^ ((r / 2) % 8)): the LDS serves 16 lanes of a 128-bit access per cycle from 64
@@ -45,8 +47,6 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kOob = 0x80000000u;
-constexpr int BM = 128;
-constexpr int kStageBytes = BM * 128;  // X: 64 bf16 of k per row
 constexpr int kWRow = 144;             // W LDS row: 128 bytes (two stages) + 16 bytes of padding
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint64_t bytes) {
@@ -68,16 +68,18 @@ __device__ __forceinline__ bf16x8 dequant8(u32x2 q, float d) {
     return __builtin_bit_cast(bf16x8, o);
 }
 
-// grid = ceil(M / 128) * ceil(N / (64 NJ)) workgroups of 512 threads. Requires K % 32 == 0,
+// grid = ceil(M / BM) * ceil(N / (64 NJ)) workgroups of 512 threads. Requires K % 32 == 0,
 // M * K * 2 < 2^31, N * K < 2^31 and the block-major scale copy in w.d.
-template <int NJ, int R>
+template <int BM, int NJ, int R>
 __global__ void __launch_bounds__(512)
 gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M) {
     static_assert(R % 2 == 0 && R >= 4, "the ring unrolls by an even R of at least 4");
-    constexpr int BN = 64 * NJ;
+    static_assert(BM == 64 || BM == 128, "64 or 128 rows");
+    constexpr int BN = 64 * NJ, TM = BM / 16, XC = BM / 64;  // row tiles, X chunks per thread
+    constexpr int kStageBytes = BM * 128;                     // X: 64 bf16 of k per row
     constexpr int kWBuf = BN * kWRow;
     constexpr int kXRegion = 3 * kStageBytes;
-    constexpr int kRedBytes = 4 * 8 * NJ * 4 * 64 * 4;  // partial tiles of the 4 second-block waves
+    constexpr int kRedBytes = 4 * TM * NJ * 4 * 64 * 4;  // partial tiles of the 4 second-block waves
     constexpr int kLds = kXRegion + 2 * kWBuf > kRedBytes ? kXRegion + 2 * kWBuf : kRedBytes;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
     const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (K + 63) / 64;
@@ -96,10 +98,10 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
 
     // X: thread t stages chunks q = t + 512 j (row q / 8, 16-byte chunk q % 8) of a stage.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint64_t)M * (uint64_t)K * 2u);
-    uint32_t xoff[2];
-    int xk[2], xlds[2];
+    uint32_t xoff[XC];
+    int xk[XC], xlds[XC];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < XC; j++) {
         const int q = tid + 512 * j, row = q >> 3, c = q & 7, gm = m0 + row;
         xoff[j] = gm < M ? (uint32_t)gm * (uint32_t)K * 2u + (uint32_t)c * 16u : kOob;
         xk[j] = c * 8;
@@ -128,7 +130,7 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
     }
 
     struct Set {
-        u32x4 x[2];
+        u32x4 x[XC];
         u32x4 q[NJ];  // loaded with even stages only: the stage pair's W bytes
         uint32_t d[NJ];
     };
@@ -139,7 +141,7 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
         const bool live = i < ns;
         const int k0 = i * 64;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < XC; j++) {
             const bool ok = live && k0 + xk[j] < K;
             S_.x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff[j] : kOob, (uint32_t)k0 * 2u, 0));
         }
@@ -157,9 +159,9 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
             S_.d[j] = __builtin_amdgcn_raw_buffer_load_b16(wd, doff[j], bok ? (uint32_t)kb * (uint32_t)N * 2u : kOob, 0);
     };
 
-    f32x4 acc[8][NJ];
+    f32x4 acc[TM][NJ];
 #pragma unroll
-    for (int t = 0; t < 8; t++)
+    for (int t = 0; t < TM; t++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     bf16x8 bfr[2][NJ];  // B operands of a stage, double-buffered
@@ -168,7 +170,7 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
     uint8_t *const wbase = lds + kXRegion;
     auto store_x = [&](const Set &S_, int buf) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) *reinterpret_cast<u32x4 *>(&xbase[buf * kStageBytes + xlds[j]]) = S_.x[j];
+        for (int j = 0; j < XC; j++) *reinterpret_cast<u32x4 *>(&xbase[buf * kStageBytes + xlds[j]]) = S_.x[j];
     };
     auto store_w = [&](const Set &S_, int wbuf) {
 #pragma unroll
@@ -184,9 +186,9 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
     // A operand of row tile t: row 16 t + lane % 16, chunk 4 kh + g (the swizzle term
     // (row / 2) % 8 does not depend on t).
     const int aoff = m16 * 128 + (((4 * kh + g) ^ ((m16 >> 1) & 7)) << 4);
-    auto read_a = [&](int buf, bf16x8 (&a)[8]) {
+    auto read_a = [&](int buf, bf16x8 (&a)[TM]) {
 #pragma unroll
-        for (int t = 0; t < 8; t++) a[t] = *reinterpret_cast<const bf16x8 *>(&xbase[buf * kStageBytes + t * 16 * 128 + aoff]);
+        for (int t = 0; t < TM; t++) a[t] = *reinterpret_cast<const bf16x8 *>(&xbase[buf * kStageBytes + t * 16 * 128 + aoff]);
     };
 
     // Prologue: stages 0 .. R-1 in flight; X of stages 0 and 1 and W of pair 0 in LDS; the
@@ -196,7 +198,7 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
         load(r, set[r], (r & 1) == 0);
         __builtin_amdgcn_sched_barrier(0);
     }
-    bf16x8 a[2][8];
+    bf16x8 a[2][TM];
     u32x2 wb[NJ];
     store_x(set[0], 0);
     store_x(set[1], 1);
@@ -229,7 +231,7 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
 #pragma unroll
             for (int j = 0; j < NJ; j++) bfr[(r + 1) & 1][j] = dequant8(wb[j], half_bits_to_float(set[(r + 1) % R].d[j]));
 #pragma unroll
-            for (int t = 0; t < 8; t++)
+            for (int t = 0; t < TM; t++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r & 1][t], bfr[r & 1][j], acc[t][j], 0, 0, 0);
             b0 = b1;
@@ -243,22 +245,22 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
     __syncthreads();  // every wave is past its last read of the stage buffers
     if (kh == 1) {
 #pragma unroll
-        for (int t = 0; t < 8; t++)
+        for (int t = 0; t < TM; t++)
 #pragma unroll
             for (int j = 0; j < NJ; j++)
 #pragma unroll
-                for (int v = 0; v < 4; v++) red[(((nw * 8 + t) * NJ + j) * 4 + v) * 64 + lane] = acc[t][j][v];
+                for (int v = 0; v < 4; v++) red[(((nw * TM + t) * NJ + j) * 4 + v) * 64 + lane] = acc[t][j][v];
     }
     __syncthreads();
     if (kh == 1) return;
 #pragma unroll
-    for (int t = 0; t < 8; t++)
+    for (int t = 0; t < TM; t++)
 #pragma unroll
         for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int row = m0 + 16 * t + 4 * g + v, col = n0 + 16 * NJ * nw + 16 * j + m16;
-                const float s = acc[t][j][v] + red[(((nw * 8 + t) * NJ + j) * 4 + v) * 64 + lane];
+                const float s = acc[t][j][v] + red[(((nw * TM + t) * NJ + j) * 4 + v) * 64 + lane];
                 if (row < M && col < N) y[(int64_t)row * N + col] = s;
             }
 }
