@@ -267,3 +267,169 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
 
 }  // namespace gw
 }  // namespace j4q
+
+namespace j4q {
+namespace gw {
+
+// Prefill GEMM, bf16 variant for small M (M <= 128): the weights are the traffic (17.8 MB
+// for N = K = 4096), so every CU streams its own 16 rows of W once over all of K, for all
+// BM rows of X (BM = 32, 64 or 128): grid = ceil(M / BM) * ceil(N / 16) workgroups of 8
+// waves. K advances in stages of 256 KPW (8 KPW Q8_0 blocks); wave w takes blocks w, w + 8,
+// ... of every stage: BM / 16 v_mfma_f32_16x16x32_bf16 accumulators of 16 columns. The 8
+// waves' partial tiles are added through LDS at the end in wave order (deterministic).
+//  - X: BM rows x 512 KPW bytes per stage through two LDS buffers, whole-line loads,
+//    16-byte chunk c of row r stored at chunk c ^ (r % 16): the 16 rows of an operand read
+//    fall on distinct banks.
+//  - W: 16 rows x 256 KPW bytes per stage through two LDS buffers of rows padded by 16
+//    bytes; each wave reads 8 bytes per lane of each of its blocks and dequantizes them to
+//    bf16(d * q) in registers, with d from the block-major scale copy.
+// One barrier per stage; global loads run R stages ahead in a ring of register sets; stages
+// past the end load zeros and add exact zeros.
+template <int BM, int KPW, int R>
+__global__ void __launch_bounds__(512)
+gemm_bf16_narrow(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M) {
+    static_assert(BM == 32 || BM == 64 || BM == 128, "32, 64 or 128 rows");
+    static_assert(KPW == 1 || KPW == 2, "one or two blocks per wave and stage");
+    static_assert(R % 2 == 0 && R >= 2, "the ring unrolls by an even R");
+    constexpr int TM = BM / 16, XC = BM * KPW / 16;  // row tiles; X chunks per thread and stage
+    constexpr int SK = 256 * KPW, XROW = 2 * SK, WROW = SK + 16;
+    constexpr int kXStage = BM * XROW, kWStage = 16 * WROW;
+    constexpr int kRed = 7 * TM * 4 * 64 * 4;  // partial tiles of waves 1..7
+    constexpr int kLds = 2 * kXStage + 2 * kWStage > kRed ? 2 * kXStage + 2 * kWStage : kRed;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (K + SK - 1) / SK;
+    const int mt = (M + BM - 1) / BM;
+    // Workgroup b runs on XCD b % 8: each XCD takes a contiguous range of tiles (m fastest).
+    const int total = (int)gridDim.x;
+    int tile = (int)blockIdx.x;
+    if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * 16;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
+
+    // X: thread t stages chunks q = t + 512 j (row q / (32 KPW), 16-byte chunk q % (32 KPW)).
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint64_t)M * (uint64_t)K * 2u);
+    uint32_t xoff[XC];
+    int xk[XC], xlds[XC];
+#pragma unroll
+    for (int j = 0; j < XC; j++) {
+        const int q = tid + 512 * j, row = q / (32 * KPW), c = q % (32 * KPW), gm = m0 + row;
+        xoff[j] = gm < M ? (uint32_t)gm * (uint32_t)K * 2u + (uint32_t)c * 16u : kOob;
+        xk[j] = c * 8;
+        xlds[j] = row * XROW + ((c ^ (row & 15)) << 4);
+    }
+    // W: thread t < 256 KPW stages chunk t (row t / (16 KPW), 16-byte chunk t % (16 KPW)) of
+    // the stage's bytes of each row; the other threads load nothing.
+    const __amdgpu_buffer_rsrc_t wq = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
+    const bool wthr = tid < 256 * KPW;
+    const int wrow = (tid / (16 * KPW)) & 15, wc = tid % (16 * KPW), wn = n0 + wrow;
+    const uint32_t woff = (wthr && wn < N) ? (uint32_t)wn * (uint32_t)K + (uint32_t)wc * 16u : kOob;
+    const int wlds = wrow * WROW + wc * 16;
+    const __amdgpu_buffer_rsrc_t wd = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
+    const uint32_t doff = n0 + m16 < N ? (uint32_t)(n0 + m16) * 2u : kOob;
+
+    struct Set {
+        u32x4 x[XC];
+        u32x4 q;
+        uint32_t d[KPW];
+    };
+    Set set[R];
+    auto load = [&](int i, Set &S_) {
+        const bool live = i < ns;
+        const int k0 = i * SK;
+#pragma unroll
+        for (int j = 0; j < XC; j++) {
+            const bool ok = live && k0 + xk[j] < K;
+            S_.x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xoff[j] : kOob, (uint32_t)k0 * 2u, 0));
+        }
+        const bool wok = live && k0 + wc * 16 < K;
+        S_.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wq, wok ? woff : kOob, (uint32_t)k0, 0));
+#pragma unroll
+        for (int j = 0; j < KPW; j++) {
+            const int kb = 8 * KPW * i + 8 * j + wave;  // this wave's blocks (wave-uniform)
+            S_.d[j] = __builtin_amdgcn_raw_buffer_load_b16(wd, doff, live && kb < nblk ? (uint32_t)kb * (uint32_t)N * 2u : kOob, 0);
+        }
+    };
+    uint8_t *const xbase = lds;
+    uint8_t *const wbase = lds + 2 * kXStage;
+    auto store = [&](const Set &S_, int buf) {
+#pragma unroll
+        for (int j = 0; j < XC; j++) *reinterpret_cast<u32x4 *>(&xbase[buf * kXStage + xlds[j]]) = S_.x[j];
+        if (wthr) *reinterpret_cast<u32x4 *>(&wbase[buf * kWStage + wlds]) = S_.q;
+    };
+    // A operand of row tile t, block j: row 16 t + lane % 16, chunk 4 (8 j + wave) + g.
+    int aoff[KPW], boff[KPW];
+#pragma unroll
+    for (int j = 0; j < KPW; j++) {
+        aoff[j] = m16 * XROW + (((4 * (8 * j + wave) + g) ^ m16) << 4);
+        boff[j] = m16 * WROW + 32 * (8 * j + wave) + 8 * g;
+    }
+
+    f32x4 acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        load(r, set[r]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    store(set[0], 0);
+    // Iteration i: the barrier publishes stage i (stored during iteration i - 1) and frees
+    // the other buffers (their last reader, stage i - 1, is done); the loads of stage i + R
+    // go into the set stage i used; stage i + 1 is stored while stage i is multiplied.
+    for (int i0 = 0; i0 < ns; i0 += R) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = i0 + r;  // i0 is a multiple of the even R: buffer i % 2 == r % 2
+            __syncthreads();
+            bf16x8 a[KPW][TM];
+            u32x2 wb[KPW];
+            float d[KPW];
+#pragma unroll
+            for (int j = 0; j < KPW; j++) {
+#pragma unroll
+                for (int t = 0; t < TM; t++) a[j][t] = *reinterpret_cast<const bf16x8 *>(&xbase[(r & 1) * kXStage + t * 16 * XROW + aoff[j]]);
+                wb[j] = *reinterpret_cast<const u32x2 *>(&wbase[(r & 1) * kWStage + boff[j]]);
+                d[j] = half_bits_to_float(set[r].d[j]);
+            }
+            load(i + R, set[r]);
+            __builtin_amdgcn_sched_barrier(0);
+            store(set[(r + 1) % R], (r + 1) & 1);
+#pragma unroll
+            for (int j = 0; j < KPW; j++) {
+                const bf16x8 b = dequant8(wb[j], d[j]);
+#pragma unroll
+                for (int t = 0; t < TM; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][t], b, acc[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- epilogue: waves 1..7 hand their partial tiles to wave 0, which adds them in wave
+    // order and stores. Result element v of row tile t is row 16 t + 4 g + v, column
+    // lane % 16.
+    float *red = reinterpret_cast<float *>(lds);
+    __syncthreads();
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) red[(((wave - 1) * TM + t) * 4 + v) * 64 + lane] = acc[t][v];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            float s = acc[t][v];
+            for (int ww = 0; ww < 7; ww++) s += red[((ww * TM + t) * 4 + v) * 64 + lane];
+            const int row = m0 + 16 * t + 4 * g + v, col = n0 + m16;
+            if (row < M && col < N) y[(int64_t)row * N + col] = s;
+        }
+}
+
+}  // namespace gw
+}  // namespace j4q
