@@ -11,12 +11,15 @@ int64_t gemv_max_cols() { return 15360; }
 namespace {
 
 // Launch shape, from measured sweeps on MI355X (one row per group, two register sets in
-// flight): for K <= 8192, 8 waves per workgroup and 2 workgroups per CU; for larger K (an
-// x image of up to 64 KiB), 16 waves in one workgroup per CU. The grid never exceeds what
-// is resident at once, so x is staged once per workgroup.
+// flight, ~62 VGPRs per wave): for K <= 4096, 8 waves per workgroup and 4 workgroups per CU
+// (8 waves per SIMD: ~5 % faster than 4, the extra waves fill the gaps the unpack leaves in
+// the memory stream); for K <= 8192, 2 workgroups per CU; for larger K (an x image of up to
+// 64 KiB), 16 waves in one workgroup per CU. The grid never exceeds what is resident at
+// once, so x is staged once per workgroup.
 template <int FMT>
 hipError_t launch_fmt(const QMat &m, const float *x, const float *add, float *y, int batch, int cus,
                       hipStream_t s) {
+    if (m.cols <= 4096) return gemv::launch<FMT, 1, 8, 2>(m, x, add, y, batch, 4 * cus, s);
     if (m.cols <= 8192) return gemv::launch<FMT, 1, 8, 2>(m, x, add, y, batch, 2 * cus, s);
     return gemv::launch<FMT, 1, 16, 2>(m, x, add, y, batch, cus, s);
 }

@@ -352,12 +352,13 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         av.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prevr, ao, 0, 0));
         av.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(addr, ao, 0, 0));
     };
-    F ta[IPW], tb[TS == 2 ? IPW : 1];
-    f32x2 aa, ab;
+    static_assert(TS == 1 || TS % 2 == 0, "tile sets: 1, or an even count (LDS partial parity)");
+    F tset[TS][IPW];
+    f32x2 avs[TS];
     const int t0 = (int)blockIdx.x, tstep = (int)gridDim.x;
     __builtin_amdgcn_sched_barrier(0);
-    load_tile(ta, aa, t0);
-    if constexpr (TS == 2) load_tile(tb, ab, t0 + tstep);
+#pragma unroll
+    for (int k = 0; k < TS; k++) load_tile(tset[k], avs[k], t0 + k * tstep);
     __builtin_amdgcn_sched_barrier(0);
     // per-batch-row factor that undoes this wave's x scale and the 2^-24 of the weights
     float wscale[BB];
@@ -513,24 +514,27 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         }
     };
 
-    // Two register sets alternate: the next tile's loads are in flight while a tile is
-    // computed and reduced. The tile loop is workgroup-uniform, so every wave reaches each
-    // barrier.
-    if constexpr (TS == 2) {
-        for (int t = t0; t < tiles; t += 2 * tstep) {
-            process(ta, aa, t, 0);
-            load_tile(ta, aa, t + 2 * tstep);
-            if (t + tstep >= tiles) break;
-            process(tb, ab, t + tstep, 1);
-            load_tile(tb, ab, t + 3 * tstep);
+    // TS register sets form a ring: the next TS - 1 tiles' loads are in flight while a tile is
+    // computed and reduced (a workgroup has only a few tiles, so with TS = 4 most of its work
+    // is requested at the start). The tile loop is workgroup-uniform, so every wave reaches
+    // each barrier.
+    if constexpr (TS >= 2) {
+        for (int t = t0; t < tiles; t += TS * tstep) {
+#pragma unroll
+            for (int k = 0; k < TS; k++) {
+                const int tk = t + k * tstep;
+                if (tk >= tiles) break;
+                process(tset[k], avs[k], tk, k & 1);
+                load_tile(tset[k], avs[k], tk + TS * tstep);
+            }
         }
     } else {
         for (int t = t0; t < tiles; t += 2 * tstep) {
-            process(ta, aa, t, 0);
+            process(tset[0], avs[0], t, 0);
             if (t + tstep >= tiles) break;
-            load_tile(ta, aa, t + tstep);
-            process(ta, aa, t + tstep, 1);
-            load_tile(ta, aa, t + 2 * tstep);
+            load_tile(tset[0], avs[0], t + tstep);
+            process(tset[0], avs[0], t + tstep, 1);
+            load_tile(tset[0], avs[0], t + 2 * tstep);
         }
     }
 }
