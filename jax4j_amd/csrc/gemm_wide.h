@@ -433,3 +433,179 @@ gemm_bf16_narrow(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, 
 
 }  // namespace gw
 }  // namespace j4q
+
+namespace j4q {
+namespace gw {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// Prefill GEMM, int8 variant: Y[m, n] = sum over blocks b, in block order, of
+// fma(float(I_b[m, n]), fl(sx[m, b] * dw[n, b]), acc) with I_b the exact int32 dot of the
+// quantized activations and the Q8_0 quants of block b. Every output is folded by one lane
+// over all of K, so results are bit-identical to a sequential fp32 loop over the blocks.
+//
+// That fold is three vector-ALU operations per output and block (convert, multiply, FMA)
+// against one v_mfma_i32_32x32x32_i8 per 32 x 32 outputs and block, so the vector ALU
+// bounds the kernel; everything else is arranged to keep it issuing. Tile 64 x 128 per
+// workgroup of 8 waves (two per SIMD); wave w owns the 32 x 32 outputs of rows 32 (w % 2),
+// columns 32 (w / 2), for all of K. K advances in stages of four blocks (128 bytes of every
+// row, one cache line):
+//  - X int8 (64 rows) and W int8 (128 rows) with whole-line loads, 128-bit LDS stores,
+//    16-byte chunk c of row r at chunk c ^ ((r / 2) % 8) of 128-byte rows, so the 16 rows of
+//    an operand read fall on distinct banks;
+//  - sx (the activation scales, [M][K / 32]): 16 bytes of each of the 64 rows per stage,
+//    loaded by wave 0 and stored block-major in LDS, so a lane's four rows of a result
+//    group are one 16-byte read;
+//  - dw from the block-major scale copy of the Q8_0 split layout, loaded by wave 1 and
+//    stored as fp32 in LDS.
+// Two LDS buffers and one barrier per stage; global loads run R stages ahead in a ring of
+// register sets. Requires K % 32 == 0, N % 8 == 0, M * K < 2^31 and N * K < 2^31.
+template <int R>
+__global__ void __launch_bounds__(512)
+gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs, float *__restrict__ y, int M) {
+    static_assert(R % 2 == 0 && R >= 2, "the ring unrolls by an even R");
+    constexpr int BM = 64, BN = 128, SB = 4;  // rows, columns, blocks per stage
+    constexpr int kXS = BM * 128, kWS = BN * 128, kSxS = SB * BM * 4, kDwS = SB * BN * 4;
+    constexpr int kBuf = kXS + kWS + kSxS + kDwS;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBuf];
+    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (nblk + SB - 1) / SB;
+    const int mt = (M + BM - 1) / BM;
+    // Workgroup b runs on XCD b % 8; each XCD takes a contiguous range of tiles (m fastest),
+    // so the m tiles of the same W rows share an L2.
+    const int total = (int)gridDim.x;
+    int tile = (int)blockIdx.x;
+    if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1, h = lane >> 5, l32 = lane & 31;
+
+    // X: thread t stages 16-byte chunk t % 8 of tile row t / 8.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xq, (uint64_t)M * (uint64_t)K);
+    const int xrow = tid >> 3, xc = tid & 7;
+    const uint32_t xoff = m0 + xrow < M ? (uint32_t)(m0 + xrow) * (uint32_t)K + (uint32_t)xc * 16u : kOob;
+    const int xlds = xrow * 128 + ((xc ^ ((xrow >> 1) & 7)) << 4);
+    // W: thread t stages chunks q = t + 512 j (tile row q / 8, chunk q % 8).
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
+    uint32_t woff[2];
+    int wlds[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int q = tid + 512 * j, row = q >> 3, c = q & 7;
+        woff[j] = n0 + row < N ? (uint32_t)(n0 + row) * (uint32_t)K + (uint32_t)c * 16u : kOob;
+        wlds[j] = kXS + row * 128 + ((c ^ ((row >> 1) & 7)) << 4);
+    }
+    // Scales: wave 0 lane r loads sx of tile row r (four blocks, 16 bytes); wave 1 lane u
+    // loads dw of block u / 16 of the stage, columns 8 (u % 16) .. + 7 (16 bytes); the
+    // block index is a per-lane offset (a buffer load's scalar offset is wave-uniform).
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(xs, (uint64_t)M * (uint64_t)nblk * 4u);
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
+    const uint32_t soff = m0 + lane < M ? (uint32_t)(m0 + lane) * (uint32_t)nblk * 4u : kOob;
+    const int dcol = 8 * (lane & 15), dblk = lane >> 4;
+    const uint32_t doff = ((uint32_t)dblk * (uint32_t)N + (uint32_t)(n0 + dcol)) * 2u;
+
+    struct Set {
+        u32x4 x, w[2], s, d;  // s: sx (wave 0 only), d: dw (wave 1 only)
+    };
+    Set set[R];
+    // Stage i covers blocks [4 i, 4 i + 4); stages at or past ns (and bytes past K) load
+    // nothing.
+    auto load = [&](int i, Set &S_) {
+        const bool live = i < ns;
+        const int kb0 = i * SB, k0 = kb0 * 32;
+        S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, live && k0 + xc * 16 < K ? xoff : kOob, (uint32_t)k0, 0));
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int c = (tid + 512 * j) & 7;
+            S_.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live && k0 + c * 16 < K ? woff[j] : kOob, (uint32_t)k0, 0));
+        }
+        // issued by every wave (the other waves' offsets are out of range and move nothing),
+        // so each set member has one definition
+        const bool sok = wave == 0 && live, dok = wave == 1 && live && kb0 + dblk < nblk && n0 + dcol < N;
+        S_.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, sok ? soff : kOob, (uint32_t)kb0 * 4u, 0));
+        S_.d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, dok ? doff : kOob, (uint32_t)kb0 * (uint32_t)N * 2u, 0));
+    };
+    auto store = [&](const Set &S_, int buf) {
+        uint8_t *const b = lds + buf * kBuf;
+        *reinterpret_cast<u32x4 *>(&b[xlds]) = S_.x;
+#pragma unroll
+        for (int j = 0; j < 2; j++) *reinterpret_cast<u32x4 *>(&b[wlds[j]]) = S_.w[j];
+        if (wave == 0) {
+            float *sx = reinterpret_cast<float *>(b + kXS + kWS) + lane;
+            const f32x4 v = __builtin_bit_cast(f32x4, S_.s);
+            sx[0 * BM] = v.x;
+            sx[1 * BM] = v.y;
+            sx[2 * BM] = v.z;
+            sx[3 * BM] = v.w;
+        } else if (wave == 1) {
+            float *dw = reinterpret_cast<float *>(b + kXS + kWS + kSxS) + dblk * BN + dcol;
+            // whole-vector casts only: this compiler's __builtin_bit_cast of one element of an
+            // ext_vector lvalue (v.y, v[i]) reads element 0
+            const f32x8 f = __builtin_convertvector(__builtin_bit_cast(f16x8, S_.d), f32x8);
+            *reinterpret_cast<f32x4 *>(dw) = __builtin_shufflevector(f, f, 0, 1, 2, 3);
+            *reinterpret_cast<f32x4 *>(dw + 4) = __builtin_shufflevector(f, f, 4, 5, 6, 7);
+        }
+    };
+    // Operand reads of block kb: A row 32 wm + lane % 32, B row 32 wn + lane % 32, chunk
+    // 2 kb + lane / 32 of the stage's 128 bytes.
+    const int ra = 32 * wm + l32, rb = 32 * wn + l32;
+    const int asw = (ra >> 1) & 7, bsw = (rb >> 1) & 7;
+    float acc[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.f;
+    auto block = [&](const uint8_t *b, int kb) {
+        const int ch = 2 * kb + h;
+        const i32x4 a = *reinterpret_cast<const i32x4 *>(&b[ra * 128 + ((ch ^ asw) << 4)]);
+        const i32x4 q = *reinterpret_cast<const i32x4 *>(&b[kXS + rb * 128 + ((ch ^ bsw) << 4)]);
+        const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[kb * BN + rb];
+        const float *sxp = reinterpret_cast<const float *>(b + kXS + kWS) + kb * BM + 32 * wm + 4 * h;
+        f32x4 sx[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) sx[i] = *reinterpret_cast<const f32x4 *>(sxp + 8 * i);
+        const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i32x16{}, 0, 0, 0);
+        // result element v: row 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], __fmul_rn(sx[v >> 2][v & 3], dw), acc[v]);
+    };
+
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        load(r, set[r]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    store(set[0], 0);
+    // Iteration i: the barrier publishes stage i (stored during iteration i - 1) and frees
+    // the other buffer (its last reader, stage i - 1, is done); the loads of stage i + R go
+    // into the set stage i came from; stage i + 1 is stored while stage i is computed.
+    for (int i0 = 0; i0 < ns; i0 += R) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = i0 + r;  // i0 is a multiple of the even R: buffer i % 2 == r % 2
+            __syncthreads();
+            load(i + R, set[r]);
+            __builtin_amdgcn_sched_barrier(0);
+            store(set[(r + 1) % R], (r + 1) & 1);
+            const uint8_t *b = lds + (r & 1) * kBuf;
+            const int kb0 = i * SB;
+            if (kb0 + SB <= nblk) {
+#pragma unroll
+                for (int kb = 0; kb < SB; kb++) block(b, kb);
+            } else {
+                for (int kb = 0; kb < SB && kb0 + kb < nblk; kb++) block(b, kb);
+            }
+        }
+    }
+    const int col = n0 + rb;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int row = m0 + 32 * wm + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (row < M && col < N) y[(int64_t)row * N + col] = acc[v];
+    }
+}
+
+}  // namespace gw
+}  // namespace j4q

@@ -29,7 +29,8 @@ TOL_ACCUM = 2e-5  # fp32 accumulation-order difference only
 # (M, N, K): tails in every dimension, one K block, the benchmark K, M above one tile. The
 # bf16 variant runs M <= 32 and 33..128 on the small-M kernel (16 weight rows per workgroup,
 # stages of 512 or 256 k: K = 32, 256 and 4096 cover a partial first stage, one stage and
-# many), 129..511 on the older 4-wave kernel.
+# many), 129..511 on the older 4-wave kernel. The int8 variant runs M <= 64 (and N % 8 != 0)
+# on the older 4-wave kernel, the rest on the 8-wave one.
 SHAPES = [(1, 32, 32), (5, 13, 256), (33, 96, 512), (128, 128, 128), (130, 257, 1024), (64, 384, 4096),
           (32, 200, 4096), (100, 48, 800)]
 
@@ -94,6 +95,24 @@ def test_gemm_bf16_matches_reference(backend, m, n, k):
     got = backend.download(y).reshape(m, n)
     assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k, bf16_weights=True)) <= TOL_ACCUM
     assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k)) <= TOL_BF16X
+    for h in (w, x, y):
+        backend.release(h)
+
+
+# The int8 variant runs M > 64 with N % 8 == 0 on the 8-wave 64 x 128 tile kernel (stages
+# of four blocks): one block; a partial last stage (K = 96, 160, 800); tails in M and N; the
+# benchmark K. Every case is bit-identical to the emulation, which folds blocks in order.
+INT8_WIDE_SHAPES = [(65, 8, 32), (512, 136, 96), (600, 1024, 4096), (2048, 256, 160), (100, 48, 800)]
+
+
+@pytest.mark.parametrize("m,n,k", INT8_WIDE_SHAPES)
+def test_gemm_int8_wide_tiles_bit_exact(backend, m, n, k):
+    note("gemm int8 wide", m, n, k)
+    w_blob, xb, w, x = upload_case(backend, m, n, k, 4000 + m + n + k)
+    y = backend.quant_matmul(w, x, "int8")
+    got = backend.download(y).reshape(m, n)
+    xq, xs = oracle.quantize_act(xb, m, k)
+    assert np.array_equal(bits(got), bits(oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k)))
     for h in (w, x, y):
         backend.release(h)
 
