@@ -24,6 +24,7 @@ namespace j4q {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -37,43 +38,45 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint6
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)n, 0x00020000);
 }
 
-// One thread per (row, 32-element block): s = amax/127, q = clamp(roundf(x * (1/s)), +-127)
-// (ggml quantize_row_q8_0 with the scale kept in fp32). Division and the reciprocal are
+// Four lanes per (row, 32-element block): s = amax/127, q = clamp(roundf(x * (1/s)), +-127)
+// (ggml quantize_row_q8_0 with the scale kept in fp32). Lane j of a quad takes elements
+// 8 j .. 8 j + 7, so a wave reads 1 KB and writes 512 bytes contiguously; the quad's maximum
+// comes from two DPP exchanges (max is exact in any order). Division and the reciprocal are
 // IEEE correctly rounded, so the result is bit-identical to a C reference.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 __global__ void __launch_bounds__(256)
-quantize_act_kernel(const uint16_t *__restrict__ x, int64_t m, int64_t k, int8_t *__restrict__ q, float *__restrict__ s) {
-    const int64_t nb = k / 32;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= m * nb) return;
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(x + t * 32);
-    float v[32];
+quantize_act_kernel(const uint16_t *__restrict__ x, int64_t n16, int8_t *__restrict__ q, float *__restrict__ s) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte chunk of x
+    const bool live = t < n16;
+    const u32x4 p = live ? reinterpret_cast<const u32x4 *>(x)[t] : u32x4{0u, 0u, 0u, 0u};
+    float v[8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const u32x4 p = src[i];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            v[8 * i + 2 * j] = __builtin_bit_cast(float, p[j] << 16);
-            v[8 * i + 2 * j + 1] = __builtin_bit_cast(float, p[j] & 0xffff0000u);
-        }
+    for (int j = 0; j < 4; j++) {
+        v[2 * j] = __builtin_bit_cast(float, p[j] << 16);
+        v[2 * j + 1] = __builtin_bit_cast(float, p[j] & 0xffff0000u);
     }
     float amax = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));  // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));  // quad_perm [2,3,0,1]
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    u32x4 out[2];
+    u32x2 out = {0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
+    for (int i = 0; i < 8; i++) {
         float r = __builtin_roundf(v[i] * id);
         r = fminf(fmaxf(r, -127.0f), 127.0f);
-        const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)r;
-        if ((i & 3) == 0) out[i >> 4][(i >> 2) & 3] = 0;
-        out[i >> 4][(i >> 2) & 3] |= b << (8 * (i & 3));
+        out[i >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * (i & 3));
     }
-    u32x4 *dst = reinterpret_cast<u32x4 *>(q + t * 32);
-    dst[0] = out[0];
-    dst[1] = out[1];
-    s[t] = d;
+    if (live) {
+        reinterpret_cast<u32x2 *>(q)[t] = out;
+        if ((threadIdx.x & 3) == 0) s[t >> 2] = d;
+    }
 }
 
 // Row index of result element v of `lane` inside a 32 x 32 MFMA tile.
@@ -381,9 +384,10 @@ gemm_kernel(QMat w, const void *__restrict__ xv, const float *__restrict__ xs, f
 }  // namespace
 
 hipError_t launch_quantize_act(const uint16_t *x, int64_t m, int64_t k, int8_t *q, float *scales, hipStream_t s) {
-    const int64_t n = m * (k / 32);
-    if (n == 0) return hipSuccess;
-    quantize_act_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(x, m, k, q, scales);
+    const int64_t n16 = m * (k / 8);  // 16-byte chunks: four per 32-element block
+    if (n16 == 0) return hipSuccess;
+    if ((n16 + 255) / 256 > 0x7fffffff) return hipErrorInvalidValue;
+    quantize_act_kernel<<<(unsigned)((n16 + 255) / 256), 256, 0, s>>>(x, n16, q, scales);
     return hipGetLastError();
 }
 

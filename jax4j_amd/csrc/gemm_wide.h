@@ -448,11 +448,14 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 // over all of K, so results are bit-identical to a sequential fp32 loop over the blocks.
 //
 // That fold is three vector-ALU operations per output and block (convert, multiply, FMA)
-// against one v_mfma_i32_32x32x32_i8 per 32 x 32 outputs and block, so the vector ALU
-// bounds the kernel; everything else is arranged to keep it issuing. Tile 64 x 128 per
-// workgroup of 8 waves (two per SIMD); wave w owns the 32 x 32 outputs of rows 32 (w % 2),
-// columns 32 (w / 2), for all of K. K advances in stages of four blocks (128 bytes of every
-// row, one cache line):
+// against one v_mfma_i32_32x32x32_i8 (16 ns per SIMD, measured) per 32 x 32 outputs and
+// block: measured on MI355X at M = 512, N = K = 4096, each of the three costs ~8.5 us of
+// a 42 us kernel, and the rest is the operand traffic (L2 to LDS to registers) that the
+// vector ALU does not hide. (Taking the scale products from the matrix core instead, as
+// a v_mfma_f32_32x32x2_f32 outer product, is exact but no faster: 29 ns per SIMD each.)
+// Tile 64 x 128 per workgroup of 8 waves (two per SIMD); wave w owns the 32 x 32 outputs of
+// rows 32 (w % 2), columns 32 (w / 2), for all of K. K advances in stages of four blocks
+// (128 bytes of every row, one cache line):
 //  - X int8 (64 rows) and W int8 (128 rows) with whole-line loads, 128-bit LDS stores,
 //    16-byte chunk c of row r at chunk c ^ ((r / 2) % 8) of 128-byte rows, so the 16 rows of
 //    an operand read fall on distinct banks;
@@ -557,17 +560,19 @@ gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs
     float acc[16];
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[v] = 0.f;
-    auto block = [&](const uint8_t *b, int kb) {
+    auto mfma = [&](const uint8_t *b, int kb) {
         const int ch = 2 * kb + h;
         const i32x4 a = *reinterpret_cast<const i32x4 *>(&b[ra * 128 + ((ch ^ asw) << 4)]);
         const i32x4 q = *reinterpret_cast<const i32x4 *>(&b[kXS + rb * 128 + ((ch ^ bsw) << 4)]);
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i32x16{}, 0, 0, 0);
+    };
+    // result element v: row 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32
+    auto fold = [&](const uint8_t *b, int kb, const i32x16 &I) {
         const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[kb * BN + rb];
         const float *sxp = reinterpret_cast<const float *>(b + kXS + kWS) + kb * BM + 32 * wm + 4 * h;
         f32x4 sx[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) sx[i] = *reinterpret_cast<const f32x4 *>(sxp + 8 * i);
-        const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i32x16{}, 0, 0, 0);
-        // result element v: row 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], __fmul_rn(sx[v >> 2][v & 3], dw), acc[v]);
     };
@@ -592,10 +597,15 @@ gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs
             const uint8_t *b = lds + (r & 1) * kBuf;
             const int kb0 = i * SB;
             if (kb0 + SB <= nblk) {
+                // the four blocks' products first: the matrix core runs them back to back
+                // while the vector ALU folds the earlier ones
+                i32x16 I[SB];
 #pragma unroll
-                for (int kb = 0; kb < SB; kb++) block(b, kb);
+                for (int kb = 0; kb < SB; kb++) I[kb] = mfma(b, kb);
+#pragma unroll
+                for (int kb = 0; kb < SB; kb++) fold(b, kb, I[kb]);
             } else {
-                for (int kb = 0; kb < SB && kb0 + kb < nblk; kb++) block(b, kb);
+                for (int kb = 0; kb < SB && kb0 + kb < nblk; kb++) fold(b, kb, mfma(b, kb));
             }
         }
     }
