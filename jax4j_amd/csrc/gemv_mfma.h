@@ -139,19 +139,25 @@ struct Fmt<Q6_K> {
     }
 };
 
-// LDS plan for BB batch rows, WAVES waves of NBW blocks each (byte offsets):
+// LDS plan for BB batch rows, WAVES waves of NBW blocks each, rounds of RT tiles (byte
+// offsets):
 //   xa   [WAVES * NBW][2 BB rows][4 lane groups][16 B]   hi/lo fp16 x image
 //   zero 512 BB bytes of zeros (A rows with no batch row read here, stride 0)
 //   cin  [WAVES * NBW][G][BB] f32                         MFMA C input per block
-//   part [2][WAVES][BB][16] f32                           per-wave partial sums
-template <int BB, int G, int WAVES, int NBW>
+//   part [RT][WAVES][BB][16] f32                          per-wave partial sums of a round
+//   pa   [RT][BB * 16] f32x2                              prev / add of a round's outputs
+template <int BB, int G, int WAVES, int NBW, int RT>
 struct Plan {
     static constexpr int kXa = 0;
     static constexpr int kZero = kXa + WAVES * NBW * 128 * BB;
     static constexpr int kCin = kZero + 512 * BB;
     static constexpr int kPart = kCin + WAVES * NBW * G * BB * 4;
-    static constexpr int kBytes = kPart + 2 * WAVES * BB * 16 * 4;
+    static constexpr int kPa = kPart + RT * WAVES * BB * 16 * 4;
+    static constexpr int kBytes = kPa + RT * BB * 16 * 8;
 };
+
+// Tiles per round (one pair of barriers per round).
+constexpr int kRound = 4;
 
 // grid: G_wg persistent workgroups of WAVES waves; workgroup w takes 16-row tiles w,
 // w + G_wg, ... The kernel covers the window of blocks [kb0, kb0 + kbn) of every row:
@@ -168,7 +174,9 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
                  int B, int kb0, int kbn) {
     using F = Fmt<FMT>;
     constexpr int S = F::S, G = F::GROUPS, NBW = IPW * S;
-    using P = Plan<BB, G, WAVES, NBW>;
+    constexpr int RT = kRound;
+    static_assert(RT % TS == 0, "a round holds whole turns of the tile ring");
+    using P = Plan<BB, G, WAVES, NBW, RT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int K = (int)m.cols, N = (int)m.rows;
     const int tiles = (N + 15) / 16, nb = kb0 + kbn;  // blocks [kb0, nb) of every row
@@ -352,7 +360,6 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         av.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prevr, ao, 0, 0));
         av.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(addr, ao, 0, 0));
     };
-    static_assert(TS == 1 || TS % 2 == 0, "tile sets: 1, or an even count (LDS partial parity)");
     F tset[TS][IPW];
     f32x2 avs[TS];
     const int t0 = (int)blockIdx.x, tstep = (int)gridDim.x;
@@ -376,7 +383,8 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
 
     // ---- 3. per tile: transpose, unpack, MFMA, block scale; partials through LDS ----------
     float *part = reinterpret_cast<float *>(lds + P::kPart);
-    auto process = [&](const F (&it)[IPW], f32x2 av, int tile, int parity) {
+    f32x2 *pa = reinterpret_cast<f32x2 *>(lds + P::kPa);
+    auto process = [&](const F (&it)[IPW], f32x2 av, int slot) {
         float acc[JB], corr[JB];
 #pragma unroll
         for (int j = 0; j < JB; j++) acc[j] = corr[j] = 0.f;
@@ -491,7 +499,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             }
         }
         // hi + lo (lanes 32..63 hold the lo rows of the batch rows in lanes 0..31)
-        float *pp = part + parity * (WAVES * BB * 16);
+        float *pp = part + slot * (WAVES * BB * 16);
 #pragma unroll
         for (int j = 0; j < JB; j++) {
             float v = acc[j] - corr[j];
@@ -503,39 +511,44 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             for (int bb = 0; bb < BB; bb++) ws = (bb == hb + j) ? wscale[bb] : ws;
             if (hi_lane) pp[(wave * BB + hb + j) * 16 + n] = v * ws;
         }
+        // the tile's prev / add values, fetched with its weights by threads (b, nn)
+        if ((int)threadIdx.x < BB * 16) pa[slot * BB * 16 + threadIdx.x] = av;
+    };
+    // End of a round of ns tiles starting at tile t: thread (k, b, nn) adds the waves'
+    // partials of output (b, row 16 (t + k tstep) + nn) in wave order. The second barrier
+    // keeps the slots until every reader is done.
+    auto finish = [&](int t, int ns) {
         __syncthreads();
-        if ((int)threadIdx.x < BB * 16) {
+        const int k = (int)threadIdx.x / (BB * 16), o = (int)threadIdx.x % (BB * 16);
+        if (k < ns) {
+            const int b = o >> 4, nn = o & 15;
+            const float *pp = part + k * (WAVES * BB * 16);
             float s = 0.f;
-            for (int w = 0; w < WAVES; w++) s += pp[(w * BB + rb) * 16 + rn];
-            const int r = tile * 16 + rn;
+            for (int w = 0; w < WAVES; w++) s += pp[(w * BB + b) * 16 + nn];
+            const f32x2 av = pa[k * BB * 16 + o];
+            const int r = (t + k * tstep) * 16 + nn;
             // the previous window's sum first, then add on its own: fl(fl(W.x) + add)
             if (prev) s += av.x;
-            if (rb < B && r < N) y[(int64_t)rb * N + r] = add ? s + av.y : s;
+            if (b < B && r < N) y[(int64_t)b * N + r] = add ? s + av.y : s;
         }
+        __syncthreads();
     };
 
     // TS register sets form a ring: the next TS - 1 tiles' loads are in flight while a tile is
-    // computed and reduced (a workgroup has only a few tiles, so with TS = 4 most of its work
-    // is requested at the start). The tile loop is workgroup-uniform, so every wave reaches
-    // each barrier.
-    if constexpr (TS >= 2) {
-        for (int t = t0; t < tiles; t += TS * tstep) {
+    // computed. Waves run through a round of RT tiles without waiting for each other; the
+    // partial sums meet at the round's end. The tile loop is workgroup-uniform, so every
+    // wave reaches each barrier.
+    for (int t = t0; t < tiles; t += RT * tstep) {
+        int ns = 0;
 #pragma unroll
-            for (int k = 0; k < TS; k++) {
-                const int tk = t + k * tstep;
-                if (tk >= tiles) break;
-                process(tset[k], avs[k], tk, k & 1);
-                load_tile(tset[k], avs[k], tk + TS * tstep);
-            }
+        for (int k = 0; k < RT; k++) {
+            const int tk = t + k * tstep;
+            if (tk >= tiles) break;
+            process(tset[k % TS], avs[k % TS], k);
+            load_tile(tset[k % TS], avs[k % TS], tk + TS * tstep);
+            ns = k + 1;
         }
-    } else {
-        for (int t = t0; t < tiles; t += 2 * tstep) {
-            process(tset[0], avs[0], t, 0);
-            if (t + tstep >= tiles) break;
-            load_tile(tset[0], avs[0], t + tstep);
-            process(tset[0], avs[0], t + tstep, 1);
-            load_tile(tset[0], avs[0], t + 2 * tstep);
-        }
+        finish(t, ns);
     }
 }
 
@@ -544,7 +557,7 @@ hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, i
                     int kb0 = 0, int kbn = -1, const float *prev = nullptr) {
     if (kbn < 0) kbn = (int)(m.cols / 32);
     constexpr int NBW = IPW * Fmt<FMT>::S;
-    constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW>::kBytes;
+    constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW, kRound>::kBytes;
     gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<grid, WAVES * 64, lds, s>>>(m, x, prev, add, y, B, kb0, kbn);
     return hipGetLastError();
 }
