@@ -68,6 +68,18 @@ __device__ __forceinline__ void xpose4(uint32_t (&v)[4]) {
     v[3] = d[1];
 }
 
+// o[t] = x of lane group t (same lane within the group), in every lane.
+__device__ __forceinline__ void bcast4(float x, float (&o)[4]) {
+    const uint32_t v = __builtin_bit_cast(uint32_t, x);
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // [g0 g1 g0 g1], [g2 g3 g2 g3]
+    const auto b0 = __builtin_amdgcn_permlane16_swap(a[0], a[0], false, false);
+    const auto b1 = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);
+    o[0] = __builtin_bit_cast(float, (uint32_t)b0[0]);
+    o[1] = __builtin_bit_cast(float, (uint32_t)b0[1]);
+    o[2] = __builtin_bit_cast(float, (uint32_t)b1[0]);
+    o[3] = __builtin_bit_cast(float, (uint32_t)b1[1]);
+}
+
 // Q4 dword of lane group g: bytes 4g..4g+3 of a 16-byte chunk (byte i: lo nibble element
 // i, hi nibble element 16 + i). Slots 0..7 of the B operand hold elements
 // 4g + {0, 2, 1, 3, 16, 18, 17, 19}; slots 4..7 carry a factor 16.
@@ -98,11 +110,12 @@ struct Fmt<Q4_K> {
     static constexpr int S = 4, GROUPS = 1;
     static constexpr float SIGMA = 0.0625f, OFF = 0.0f;
     u32x4 q;
-    u32x4 meta;  // superblock: d | dmin | D0 | D1 | D2 (split layout, j4q_common.h)
+    // superblock header d | dmin | D0 | D1 | D2 (split layout, j4q_common.h): loaded once per
+    // tile, into item 0 (see load_tile)
+    u32x4 meta;
     __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
-        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob, so_s = live ? (uint32_t)(blk0 >> 3) * 16u : kOob;
+        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob;
         q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
-        meta = ld128(r.sc, row * (K / 16u), so_s);
     }
 };
 
@@ -124,18 +137,16 @@ struct Fmt<Q6_K> {
     static constexpr int S = 4, GROUPS = 2;
     static constexpr float SIGMA = 0.0625f, OFF = 32.0f;
     u32x4 q;
-    u32x2 h;   // qh of chunk g (two dwords)
-    u32x2 sc;  // int8 group scales of chunks 0..3
-    uint32_t d;
+    u32x2 h;  // qh of chunk g (two dwords)
+    // per tile, in item 0 (see load_tile): the int8 group scales of the wave's 16 blocks
+    // (32 bytes) and the fp16 d of its two superblocks
+    u32x4 sca, scb;
+    uint32_t dd;
     __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
         const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob;
         const uint32_t so_h = live ? (uint32_t)blk0 * 8u : kOob;
-        const uint32_t so_s = live ? (uint32_t)blk0 * 2u : kOob;
-        const uint32_t so_d = live ? (uint32_t)(blk0 >> 3) * 2u : kOob;
         q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
         h = ld64(r.qh, row * (K / 4u) + 8u * g, so_h);
-        sc = ld64(r.sc, row * (K / 16u), so_s);
-        d = gemv::ld16(r.d, row * (K / 128u), so_d);
     }
 };
 
@@ -343,6 +354,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     // Q4_0 scales: one load per tile, lane group g fetching item g's four (16 rows x 32 B
     // instead of 16 rows x 8 B per item); process() broadcasts them across the groups.
     static_assert(FMT != Q4_0 || IPW <= 4, "Q4_0 tile scales cover four items");
+    static_assert((FMT != Q4_K && FMT != Q6_K) || IPW * F::S == 16, "Q4_K, Q6_K: a wave's slice is two superblocks");
     auto load_tile = [&](F (&it)[IPW], f32x2 &av, int tile) {
         const bool live = tile < tiles;
         const int r = tile * 16 + n;
@@ -353,6 +365,24 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         if constexpr (FMT == Q4_0) {
             const bool ok = live && g < IPW && blkw + g * S < nb;
             it[0].d = ld64(rs.sc, row * (uint32_t)(K / 16) + 8u * (uint32_t)g, ok ? (uint32_t)blkw * 2u : kOob);
+        }
+        // Q4_K: the wave's slice spans two superblocks; lane groups 0, 1 fetch the header of
+        // the first, 2, 3 that of the second (16 rows x 32 contiguous bytes in one load)
+        // Q6_K: every lane fetches its row's scales of the slice (two 16-byte loads) and both
+        // superblock scales: four loads per tile instead of two per item
+        if constexpr (FMT == Q6_K) {
+            const uint32_t so = live ? (uint32_t)blkw * 2u : kOob;
+            it[0].sca = ld128(rs.sc, row * (uint32_t)(K / 16), so);
+            it[0].scb = ld128(rs.sc, row * (uint32_t)(K / 16) + 16u, so);
+            // two 16-bit loads: a row's d section (K / 128 bytes) is only 2-byte aligned
+            const uint32_t so_d = live ? (uint32_t)(blkw >> 3) * 2u : kOob;
+            it[0].dd = gemv::ld16(rs.d, row * (uint32_t)(K / 128), so_d) |
+                       (gemv::ld16(rs.d, row * (uint32_t)(K / 128) + 2u, so_d) << 16);
+        }
+        if constexpr (FMT == Q4_K) {
+            const uint32_t hs = (uint32_t)g >> 1;
+            const bool ok = live && blkw + 8 * (int)hs < nb;
+            it[0].meta = ld128(rs.sc, row * (uint32_t)(K / 16) + 16u * hs, ok ? (uint32_t)(blkw >> 3) * 16u : kOob);
         }
         const int ar = tile * 16 + rn;
         const bool aok = live && (int)threadIdx.x < 16 * BB && rb < B && ar < N;
@@ -388,6 +418,22 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         float acc[JB], corr[JB];
 #pragma unroll
         for (int j = 0; j < JB; j++) acc[j] = corr[j] = 0.f;
+        // Q4_K: the min terms sum_blocks dmin * m * sum(x') as a 16 x 16 x 4 fp32 MFMA per
+        // item (A: block sums of the hi batch rows, B: dmin * m of each row's 4 blocks), in
+        // the result layout of the block products
+        f32x4 corr4 = {0.f, 0.f, 0.f, 0.f};
+        // Q4_K: both superblock headers of the slice in every lane: one swap of the lane
+        // halves per dword (hdr[0] from groups 0, 1; hdr[1] from groups 2, 3)
+        uint32_t hdr[2][4] = {};
+        if constexpr (FMT == Q4_K) {
+            const uint32_t m4[4] = {it[0].meta.x, it[0].meta.y, it[0].meta.z, it[0].meta.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(m4[k], m4[k], false, false);
+                hdr[0][k] = sw[0];
+                hdr[1][k] = sw[1];
+            }
+        }
         // Q4_0: item i's scales live in lane group i of it[0].d; broadcast them to all groups
         uint32_t bd[4][2];
         if constexpr (FMT == Q4_0) {
@@ -409,6 +455,19 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             if constexpr (FMT == Q4_0 || FMT == Q4_K) {
                 uint32_t v[4] = {it[i].q.x, it[i].q.y, it[i].q.z, it[i].q.w};
                 xpose4(v);
+                // Q4_K: lane group g decodes the scale and min of block g of the item; the
+                // scales go to every group, the mins feed the min-term MFMA in place
+                float dsck[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (FMT == Q4_K) {
+                    const uint32_t *mt = hdr[(i * S) >> 3];
+                    const int sj = (blk0 & 7) + g;
+                    const f32x2 dm2 = __builtin_convertvector(__builtin_bit_cast(h2, mt[0]), f32x2);
+                    const uint32_t scj = __builtin_amdgcn_ubfe(mt[1], 4 * sj, 4) | (__builtin_amdgcn_ubfe(mt[3], 2 * sj, 2) << 4);
+                    const uint32_t mnj = __builtin_amdgcn_ubfe(mt[2], 4 * sj, 4) | (__builtin_amdgcn_ubfe(mt[3], 16 + 2 * sj, 2) << 4);
+                    bcast4(dm2.x * (float)scj, dsck);
+                    const float sa = mrow < BB ? reinterpret_cast<const float *>(lds + P::kCin)[(lw + i * S + g) * BB + mrow] : 0.f;
+                    corr4 = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, dm2.y * (float)mnj, corr4, 0, 0, 0);
+                }
                 f32x4 c[4];
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
@@ -422,25 +481,14 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
                 }
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    const int bl = i * S + t;
                     if constexpr (FMT == Q4_0) {
                         const uint32_t dw = bd[i][t >> 1];
                         const float df = (float)__builtin_bit_cast(h2, dw)[t & 1];
 #pragma unroll
                         for (int j = 0; j < JB; j++) acc[j] = __builtin_fmaf(df, c[t][j], acc[j]);
                     } else {
-                        const u32x4 mt = it[i].meta;
-                        const int sj = (blk0 & 7) + t;
-                        const float dd = (float)__builtin_bit_cast(h2, mt.x)[0];
-                        const float dm = (float)__builtin_bit_cast(h2, mt.x)[1];
-                        const uint32_t scj = __builtin_amdgcn_ubfe(mt.y, 4 * sj, 4) | (__builtin_amdgcn_ubfe(mt.w, 2 * sj, 2) << 4);
-                        const uint32_t mnj = __builtin_amdgcn_ubfe(mt.z, 4 * sj, 4) | (__builtin_amdgcn_ubfe(mt.w, 16 + 2 * sj, 2) << 4);
-                        const float dsc = dd * (float)scj, dmn = dm * (float)mnj;
 #pragma unroll
-                        for (int j = 0; j < JB; j++) {
-                            acc[j] = __builtin_fmaf(dsc, c[t][j], acc[j]);
-                            corr[j] = __builtin_fmaf(dmn, C(bl, j), corr[j]);
-                        }
+                        for (int j = 0; j < JB; j++) acc[j] = __builtin_fmaf(dsck[t], c[t][j], acc[j]);
                     }
                 }
             } else if constexpr (FMT == Q8_0) {
@@ -468,7 +516,10 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
                 const auto e0 = __builtin_amdgcn_permlane16_swap(hs[0], hs[0], false, false);
                 const auto e1 = __builtin_amdgcn_permlane16_swap(hs[1], hs[1], false, false);
                 const uint32_t hq[4] = {e0[0], e0[1], e1[0], e1[1]};
-                const float df = (float)__builtin_bit_cast(_Float16, (uint16_t)(it[i].d & 0xFFFFu));
+                const float df = (float)__builtin_bit_cast(_Float16, (uint16_t)(it[0].dd >> (16 * ((i * S) >> 3))));
+                // scale dwords 2 i, 2 i + 1 of the slice's eight
+                const uint32_t sc2[2] = {i < 2 ? it[0].sca[(2 * i) & 3] : it[0].scb[(2 * i) & 3],
+                                         i < 2 ? it[0].sca[(2 * i + 1) & 3] : it[0].scb[(2 * i + 1) & 3]};
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     const int bl = i * S + t;
@@ -490,7 +541,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
                                                                __builtin_bit_cast(h4, u32x2{p0, p2}), c0, 0, 0, 0);
                     c1 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(aop, aop, 4, 5, 6, 7),
                                                                __builtin_bit_cast(h4, u32x2{p1, p3}), c1, 0, 0, 0);
-                    const uint32_t scw = t < 2 ? it[i].sc.x : it[i].sc.y;
+                    const uint32_t scw = sc2[t >> 1];
                     const float s0 = df * (float)(int8_t)(scw >> (16 * (t & 1))),
                                 s1 = df * (float)(int8_t)(scw >> (16 * (t & 1) + 8));
 #pragma unroll
@@ -502,7 +553,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         float *pp = part + slot * (WAVES * BB * 16);
 #pragma unroll
         for (int j = 0; j < JB; j++) {
-            float v = acc[j] - corr[j];
+            float v = acc[j] - (FMT == Q4_K ? corr4[j] : corr[j]);
             const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
                                                              __builtin_bit_cast(uint32_t, v), false, false);
             v += __builtin_bit_cast(float, (uint32_t)sw[1]);
