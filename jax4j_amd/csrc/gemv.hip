@@ -45,7 +45,11 @@ hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y
     const int grid = tiles < g_cus ? tiles : g_cus;
     const int nb = (int)(m.cols / 32);
     const int windows = (nb + CAP - 1) / CAP;
-    const int per = ((nb + windows - 1) / windows + S - 1) / S * S;  // equal windows, S-aligned
+    // equal windows, aligned to whole items (K-quants: to whole 8-block superblocks, so each
+    // wave's slice starts a superblock)
+    constexpr int AL = FMT == Q4_K || FMT == Q6_K ? 8 : S;
+    static_assert(CAP % AL == 0, "windows fit the cap");
+    const int per = ((nb + windows - 1) / windows + AL - 1) / AL * AL;
     for (int kb0 = 0; kb0 < nb; kb0 += per) {
         const int kbn = nb - kb0 < per ? nb - kb0 : per;
         const bool last = kb0 + kbn >= nb;

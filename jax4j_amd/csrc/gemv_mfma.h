@@ -176,9 +176,10 @@ constexpr int kRound = 4;
 // prev (each adding the previous window's y, read before that element is rewritten) and
 // the caller's add joins only in the last window.
 // Wave v owns window blocks [v NBW, (v + 1) NBW) (NBW = IPW * S); blocks past the window
-// load nothing and their x image is zero. Requires kb0 and kbn multiples of S,
-// kbn <= WAVES * NBW and B <= BB. XREG keeps the wave's A operands and C inputs in
-// registers for the whole kernel instead of re-reading them from LDS per tile.
+// load nothing and their x image is zero. Requires kb0 and kbn multiples of S (Q4_K, Q6_K:
+// of 8, so every slice starts on a superblock), kbn <= WAVES * NBW and B <= BB. XREG keeps
+// the wave's A operands and C inputs in registers for the whole kernel instead of
+// re-reading them from LDS per tile.
 template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS>
 __global__ void __launch_bounds__(WAVES * 64)
 gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const float *__restrict__ add, float *y,

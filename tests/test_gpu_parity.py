@@ -237,9 +237,12 @@ def test_gemv_batched_matches_oracle(backend, uploaded, qt, rows, cols, B):
 # K above one 4096-column launch window: the batched kernel runs equal windows, each adding
 # the previous window's y, and the caller's add joins only in the last one (11008 = three
 # windows of 116, 116 and 112 blocks; 14336 = four of 112).
+# K = 11008 for the K-quants gives 344 blocks in three windows that must start on
+# superblocks (120-block windows, not 116)
 WIDE_CASES = [
     (QuantType.Q4_0, 700, 11008), (QuantType.Q8_0, 300, 8192),
     (QuantType.Q4_K, 300, 12288), (QuantType.Q6_K, 512, 14336),
+    (QuantType.Q4_K, 200, 11008), (QuantType.Q6_K, 136, 11008),
 ]
 
 
