@@ -26,20 +26,24 @@ hipError_t launch_fmt(const QMat &m, const float *x, const float *add, float *y,
 
 int g_cus = 256;
 
-// Blocks per launch window of launch_mfma: 8 waves x items per wave x tile sets, 128
-// blocks (4096 columns) for every format.
-template <int FMT>
-constexpr int mfma_window() { return FMT == Q8_0 ? 8 * 8 * 2 : 8 * 4 * 4; }
+// Items per wave of launch_mfma: 8 waves x items x blocks per item is the launch window,
+// 128 blocks (4096 columns) for up to 8 batch rows; 64 blocks at 16 rows, whose x image of
+// 16 rows x 4096 columns would not fit in LDS.
+template <int FMT, int BB>
+constexpr int mfma_ipw() { return (FMT == Q8_0 ? 8 : 4) / (BB > 8 ? 2 : 1); }
+template <int FMT, int BB>
+constexpr int mfma_window() { return 8 * mfma_ipw<FMT, BB>() * (FMT == Q8_0 ? 2 : 4); }
 
-// Batched GEMV on the matrix cores (gemv_mfma.h) for up to 8 batch rows per launch:
+// Batched GEMV on the matrix cores (gemv_mfma.h) for up to 16 batch rows per launch:
 // persistent grid of one 8-wave workgroup per CU, each launch a window of up to 128 blocks
-// (4096 columns) split into 8 wave slices; a wider K runs as equal windows, each adding the
-// previous window's output. Measured on MI355X (Q4_0 11008 x 4096): B = 4 11.8 us, B = 8
-// 13.1 us, against 22 us and 41 us for one vector-ALU pass per batch row; at B <= 2 the
-// two are level.
+// (4096 columns; 64 at 16 rows) split into 8 wave slices; a wider K runs as equal windows,
+// each adding the previous window's output. Measured on MI355X (Q4_0 11008 x 4096): B = 4
+// 10.8 us, B = 8 12.4 us, against 22 us and 41 us for one vector-ALU pass per batch row;
+// at B <= 2 the two are level. The Llama-3-8B decode step at B = 16 takes 4.8 ms with one
+// 16-row pass per matrix, 6.1 ms with two 8-row passes.
 template <int FMT, int BB>
 hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
-    constexpr int IPW = FMT == Q8_0 ? 8 : 4, S = FMT == Q8_0 ? 2 : 4, CAP = mfma_window<FMT>();
+    constexpr int IPW = mfma_ipw<FMT, BB>(), S = FMT == Q8_0 ? 2 : 4, CAP = mfma_window<FMT, BB>();
     static_assert(CAP == 8 * IPW * S, "window = waves x items per wave x tile sets");
     const int tiles = (int)((m.rows + 15) / 16);
     const int grid = tiles < g_cus ? tiles : g_cus;
@@ -62,14 +66,19 @@ hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y
 
 template <int FMT>
 hipError_t launch_mfma_fmt(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
-    return b <= 4 ? launch_mfma<FMT, 4>(m, x, add, y, b, s) : launch_mfma<FMT, 8>(m, x, add, y, b, s);
+    if (b <= 4) return launch_mfma<FMT, 4>(m, x, add, y, b, s);
+    if (b <= 8) return launch_mfma<FMT, 8>(m, x, add, y, b, s);
+    return launch_mfma<FMT, 16>(m, x, add, y, b, s);
 }
+
+// Several windows read add only in the last one, after y was rewritten: an add that
+// overlaps y then keeps a single window (or the single-pass vector-ALU kernel).
+template <int BB>
+bool single_window(const QMat &m) { return m.cols <= 32 * mfma_window<Q4_0, BB>(); }
 
 bool mfma_supported(int id, const QMat &m, bool add_aliases_y) {
     const int64_t k = m.cols;
-    // several windows read add only in the last one, after y was rewritten: an add that
-    // overlaps y then keeps the single-pass vector-ALU kernel
-    if (add_aliases_y && k > 32 * mfma_window<Q4_0>()) return false;
+    if (add_aliases_y && !single_window<8>(m)) return false;
     switch (id) {
     case Q4_0: case Q4_K: case Q6_K: return k % 128 == 0;
     case Q8_0: return k % 64 == 0;
@@ -108,10 +117,12 @@ hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, 
     if (m.cols > gemv_max_cols() || batch > 65535 || m.rows > (1 << 30)) return hipErrorInvalidValue;
     const bool alias = add && add < y + batch * m.rows && y < add + batch * m.rows;
     if (batch < 3 || !mfma_supported(id, m, alias)) return launch_valu(id, m, x, add, y, (int)batch, s);
-    // batch rows in launches of up to 8 on the matrix cores; a remainder of 1 or 2 rows
-    // takes the vector-ALU kernel, which is as fast there
+    // batch rows in launches of up to 16 on the matrix cores (9..16 rows stream W once, in
+    // windows of 2048 columns); a remainder of 1 or 2 rows takes the vector-ALU kernel,
+    // which is as fast there
+    const int64_t cap = !alias || single_window<16>(m) ? 16 : 8;
     for (int64_t b0 = 0; b0 < batch;) {
-        const int64_t nb = batch - b0 < 8 ? batch - b0 : 8;
+        const int64_t nb = batch - b0 < cap ? batch - b0 : cap;
         const float *xb = x + b0 * m.cols;
         const float *ab = add ? add + b0 * m.rows : nullptr;
         float *yb = y + b0 * m.rows;

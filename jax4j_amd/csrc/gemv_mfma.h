@@ -1,5 +1,5 @@
 // Batched decode GEMV on the matrix cores: y[b][n] = sum_k W[n, k] x[b][k] (+ add[b][n]) for
-// a batch of B <= 8 activation rows, split-layout weights, with W streamed once for the batch.
+// a batch of B <= 16 activation rows, split-layout weights, with W streamed once for the batch.
 //
 // The vector-ALU GEMV (gemv_impl.h) streams W once per batch row: at B = 8 it reads every
 // weight eight times. Here the products run on v_mfma_f32_16x16x32_f16 (16x16x16 for
@@ -13,10 +13,12 @@
 //    subnormals exactly, and products are exact in its fp32 accumulator.
 //  - Activations: per batch row and wave, x is scaled by a power of two 2^e (max |x| * 2^e
 //    over the wave's K slice in [2^14, 2^15), so nothing overflows fp16) and split into
-//    x' = hi + lo, two fp16 values carrying 22 significant bits. The A operand's 16 rows
-//    hold hi of batch rows 0..7 (rows 0..7) and lo (rows 8..15); rows without a batch row
-//    are zero. A wave's partial sums are multiplied by 2^(24 - e) before the waves' sums
-//    are added, so each wave may pick its own e.
+//    x' = hi + lo, two fp16 values carrying 22 significant bits. For up to 8 batch rows the
+//    A operand's 16 rows hold hi of batch rows 0..7 (rows 0..7) and lo (rows 8..15); rows
+//    without a batch row are zero. For 16 batch rows there are two A operands (hi, lo) and
+//    the lo MFMA takes the hi one's result as its C input. A wave's partial sums are
+//    multiplied by 2^(24 - e) before the waves' sums are added, so each wave may pick its
+//    own e.
 //  - Offsets: the MFMA's C input carries -OFF * 2^-24 * sum(x') of the block, so the C
 //    output is 2^-24 * sum (q - OFF) x' and one FMA with the block scale folds it into
 //    the fp32 accumulator (Q4_K's min term is a second FMA).
@@ -153,7 +155,8 @@ struct Fmt<Q6_K> {
 // LDS plan for BB batch rows, WAVES waves of NBW blocks each, rounds of RT tiles (byte
 // offsets):
 //   xa   [WAVES * NBW][2 BB rows][4 lane groups][16 B]   hi/lo fp16 x image
-//   zero 512 BB bytes of zeros (A rows with no batch row read here, stride 0)
+//   zero 512 BB bytes of zeros (A rows with no batch row read here, stride 0; none at
+//        BB = 16, where every row carries one)
 //   cin  [WAVES * NBW][G][BB] f32                         MFMA C input per block
 //   part [RT][WAVES][BB][16] f32                          per-wave partial sums of a round
 //   pa   [RT][BB * 16] f32x2                              prev / add of a round's outputs
@@ -161,14 +164,15 @@ template <int BB, int G, int WAVES, int NBW, int RT>
 struct Plan {
     static constexpr int kXa = 0;
     static constexpr int kZero = kXa + WAVES * NBW * 128 * BB;
-    static constexpr int kCin = kZero + 512 * BB;
+    static constexpr int kCin = kZero + (BB <= 8 ? 512 * BB : 0);
     static constexpr int kPart = kCin + WAVES * NBW * G * BB * 4;
     static constexpr int kPa = kPart + RT * WAVES * BB * 16 * 4;
     static constexpr int kBytes = kPa + RT * BB * 16 * 8;
 };
 
-// Tiles per round (one pair of barriers per round).
-constexpr int kRound = 4;
+// Tiles per round (one pair of barriers per round): 4, or 2 at BB = 16 (LDS).
+template <int BB>
+constexpr int round_tiles() { return BB <= 8 ? 4 : 2; }
 
 // grid: G_wg persistent workgroups of WAVES waves; workgroup w takes 16-row tiles w,
 // w + G_wg, ... The kernel covers the window of blocks [kb0, kb0 + kbn) of every row:
@@ -186,7 +190,9 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
                  int B, int kb0, int kbn) {
     using F = Fmt<FMT>;
     constexpr int S = F::S, G = F::GROUPS, NBW = IPW * S;
-    constexpr int RT = kRound;
+    constexpr bool W16 = BB == 16;  // two A operands (hi, lo) of 16 batch rows each
+    static_assert(BB <= 8 || (W16 && !XREG), "BB up to 8, or 16 without XREG");
+    constexpr int RT = round_tiles<BB>();
     static_assert(RT % TS == 0, "a round holds whole turns of the tile ring");
     using P = Plan<BB, G, WAVES, NBW, RT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -220,7 +226,8 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     }
     // zero block for the A rows and C inputs that carry no batch row (every wave writes the
     // same zeros, so no wave depends on another)
-    for (int i = lane; i < 128 * BB; i += 64) reinterpret_cast<uint32_t *>(lds + P::kZero)[i] = 0u;
+    if constexpr (!W16)
+        for (int i = lane; i < 128 * BB; i += 64) reinterpret_cast<uint32_t *>(lds + P::kZero)[i] = 0u;
     float sx[BB];
     int ex[BB];
     {
@@ -314,9 +321,15 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     // batch row m - 8, other rows read the zero block with stride 0. The C rows of lane
     // group g are 4g..4g+3: groups 0 and 1 hold the hi rows of batch rows 4 (g & 1) + j and
     // take the C inputs; groups 2 and 3 hold the lo rows and read zeros.
+    // BB = 16: row m of the first A operand is hi of batch row m, of the second lo of batch
+    // row m; the second MFMA takes the first one's result as its C input, so every C row
+    // 4g + j is batch row 4g + j (hi + lo) and every lane group takes the C inputs.
     const int mrow = lane & 15;
     int abase, astride;
-    if (mrow < BB) {
+    if constexpr (W16) {
+        abase = P::kXa + ((lw * 2 * BB + mrow) * 4 + g) * 16;
+        astride = 128 * BB;
+    } else if (mrow < BB) {
         abase = P::kXa + ((lw * 2 * BB + mrow) * 4 + g) * 16;
         astride = 128 * BB;
     } else if (mrow >= 8 && mrow < 8 + BB) {
@@ -327,11 +340,13 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         astride = 0;
     }
     constexpr int JB = BB < 4 ? BB : 4;  // C rows per lane that carry a batch row
-    const int hb = 4 * (g & 1);          // first batch row of this lane's C rows
-    const bool hi_lane = g < 2 && hb < BB;
+    const int hb = W16 ? 4 * g : 4 * (g & 1);  // first batch row of this lane's C rows
+    const bool hi_lane = W16 || (g < 2 && hb < BB);
     const int cbase = hi_lane ? P::kCin + (lw * G * BB + hb) * 4 : P::kZero;
     const int cstride = hi_lane ? G * BB * 4 : 0;
     auto a_op = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + bl * astride); };
+    // BB = 16: the lo operand, BB rows further on in the block's image
+    auto a_lo = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + BB * 64 + bl * astride); };
     auto c_in = [&](int bl, int k) { return reinterpret_cast<const float *>(lds + cbase + bl * cstride)[k]; };
     // registers keep only this lane's C inputs: k = j (group 0) and k = BB + j (Q6_K group 1)
     h8 areg[XREG ? NBW : 1];
@@ -355,7 +370,8 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     // Q4_0 scales: one load per tile, lane group g fetching item g's four (16 rows x 32 B
     // instead of 16 rows x 8 B per item); process() broadcasts them across the groups.
     static_assert(FMT != Q4_0 || IPW <= 4, "Q4_0 tile scales cover four items");
-    static_assert((FMT != Q4_K && FMT != Q6_K) || IPW * F::S == 16, "Q4_K, Q6_K: a wave's slice is two superblocks");
+    static_assert((FMT != Q4_K && FMT != Q6_K) || IPW * F::S == 16 || IPW * F::S == 8,
+                  "Q4_K, Q6_K: a wave's slice is one or two superblocks");
     auto load_tile = [&](F (&it)[IPW], f32x2 &av, int tile) {
         const bool live = tile < tiles;
         const int r = tile * 16 + n;
@@ -367,8 +383,6 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             const bool ok = live && g < IPW && blkw + g * S < nb;
             it[0].d = ld64(rs.sc, row * (uint32_t)(K / 16) + 8u * (uint32_t)g, ok ? (uint32_t)blkw * 2u : kOob);
         }
-        // Q4_K: the wave's slice spans two superblocks; lane groups 0, 1 fetch the header of
-        // the first, 2, 3 that of the second (16 rows x 32 contiguous bytes in one load)
         // Q6_K: every lane fetches its row's scales of the slice (two 16-byte loads) and both
         // superblock scales: four loads per tile instead of two per item
         if constexpr (FMT == Q6_K) {
@@ -380,6 +394,8 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             it[0].dd = gemv::ld16(rs.d, row * (uint32_t)(K / 128), so_d) |
                        (gemv::ld16(rs.d, row * (uint32_t)(K / 128) + 2u, so_d) << 16);
         }
+        // Q4_K: the wave's slice spans up to two superblocks; lane groups 0, 1 fetch the
+        // header of the first, 2, 3 that of the second (16 rows x 32 contiguous bytes in one load)
         if constexpr (FMT == Q4_K) {
             const uint32_t hs = (uint32_t)g >> 1;
             const bool ok = live && blkw + 8 * (int)hs < nb;
@@ -478,7 +494,9 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
 #pragma unroll
                         for (int j = 0; j < JB; j++) c[t][j] = C(bl, j);
                     }
-                    c[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A(bl), __builtin_bit_cast(h8, q4_slots(v[t])), c[t], 0, 0, 0);
+                    const h8 bq = __builtin_bit_cast(h8, q4_slots(v[t]));
+                    c[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A(bl), bq, c[t], 0, 0, 0);
+                    if constexpr (W16) c[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo(bl), bq, c[t], 0, 0, 0);
                 }
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
@@ -504,6 +522,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
 #pragma unroll
                     for (int j = 0; j < JB; j++) c[j] = C(bl, j);
                     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A(bl), __builtin_bit_cast(h8, sl), c, 0, 0, 0);
+                    if constexpr (W16) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo(bl), __builtin_bit_cast(h8, sl), c, 0, 0, 0);
                     const float df = (float)__builtin_bit_cast(h2, it[i].d)[t];
 #pragma unroll
                     for (int j = 0; j < JB; j++) acc[j] = __builtin_fmaf(df, c[j], acc[j]);
@@ -538,10 +557,14 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
                         c0[j] = C(bl, j);
                         c1[j] = C(bl, BB + j);
                     }
-                    c0 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(aop, aop, 0, 1, 2, 3),
-                                                               __builtin_bit_cast(h4, u32x2{p0, p2}), c0, 0, 0, 0);
-                    c1 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(aop, aop, 4, 5, 6, 7),
-                                                               __builtin_bit_cast(h4, u32x2{p1, p3}), c1, 0, 0, 0);
+                    const h4 b0 = __builtin_bit_cast(h4, u32x2{p0, p2}), b1 = __builtin_bit_cast(h4, u32x2{p1, p3});
+                    c0 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(aop, aop, 0, 1, 2, 3), b0, c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(aop, aop, 4, 5, 6, 7), b1, c1, 0, 0, 0);
+                    if constexpr (W16) {
+                        const h8 alo = a_lo(bl);
+                        c0 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(alo, alo, 0, 1, 2, 3), b0, c0, 0, 0, 0);
+                        c1 = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_shufflevector(alo, alo, 4, 5, 6, 7), b1, c1, 0, 0, 0);
+                    }
                     const uint32_t scw = sc2[t >> 1];
                     const float s0 = df * (float)(int8_t)(scw >> (16 * (t & 1))),
                                 s1 = df * (float)(int8_t)(scw >> (16 * (t & 1) + 8));
@@ -550,14 +573,16 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
                 }
             }
         }
-        // hi + lo (lanes 32..63 hold the lo rows of the batch rows in lanes 0..31)
+        // hi + lo (BB <= 8: lanes 32..63 hold the lo rows of the batch rows in lanes 0..31)
         float *pp = part + slot * (WAVES * BB * 16);
 #pragma unroll
         for (int j = 0; j < JB; j++) {
             float v = acc[j] - (FMT == Q4_K ? corr4[j] : corr[j]);
-            const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
-                                                             __builtin_bit_cast(uint32_t, v), false, false);
-            v += __builtin_bit_cast(float, (uint32_t)sw[1]);
+            if constexpr (!W16) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                                 __builtin_bit_cast(uint32_t, v), false, false);
+                v += __builtin_bit_cast(float, (uint32_t)sw[1]);
+            }
             float ws = 0.f;
 #pragma unroll
             for (int bb = 0; bb < BB; bb++) ws = (bb == hb + j) ? wscale[bb] : ws;
@@ -609,7 +634,8 @@ hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, i
                     int kb0 = 0, int kbn = -1, const float *prev = nullptr) {
     if (kbn < 0) kbn = (int)(m.cols / 32);
     constexpr int NBW = IPW * Fmt<FMT>::S;
-    constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW, kRound>::kBytes;
+    constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW, round_tiles<BB>()>::kBytes;
+    static_assert(lds <= 160 * 1024, "LDS of one workgroup");
     gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<grid, WAVES * 64, lds, s>>>(m, x, prev, add, y, B, kb0, kbn);
     return hipGetLastError();
 }
