@@ -403,12 +403,20 @@ hipError_t launch_gemm(const QMat &w, const void *x, const float *xs, float *y, 
 hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs, float *y, int64_t m, hipStream_t s) {
     if (m <= 0 || w.rows <= 0) return hipSuccess;
     if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols > 0x7fffffffull) return hipErrorInvalidValue;
-    if (m > 64 && w.rows % 8 == 0 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
-        // gemm_wide.h: 64 x 128 tiles of 8 waves (measured on MI355X, N = K = 4096: M = 128
-        // 36.0 us against 48.6, M = 512 40.2 against 52.0, M = 2048 151 against 181)
-        const int64_t tiles = ((m + 63) / 64) * ((w.rows + 127) / 128);
-        if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-        gw::gemm_i8_wide<4><<<(unsigned)tiles, 512, 0, s>>>(w, xq, xs, y, (int)m);
+    if (w.rows % 8 == 0 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
+        // gemm_wide.h, measured on MI355X at N = K = 4096: 16 x 32 tiles of 2 waves up to
+        // M = 256 (M = 32 16.8 us against 33.1 on the 4-wave kernel, M = 128 23.3 against 36.0,
+        // M = 256 35.0 against 37.0), 64 x 128 tiles of 8 waves above (M = 512 40.2 us against
+        // 52.0, M = 2048 151 against 181)
+        if (m <= 256) {
+            const int64_t tiles = ((m + 15) / 16) * ((w.rows + 31) / 32);
+            if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+            gw::gemm_i8_small<4><<<(unsigned)tiles, 128, 0, s>>>(w, xq, xs, y, (int)m);
+        } else {
+            const int64_t tiles = ((m + 63) / 64) * ((w.rows + 127) / 128);
+            if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+            gw::gemm_i8_wide<4><<<(unsigned)tiles, 512, 0, s>>>(w, xq, xs, y, (int)m);
+        }
         return hipGetLastError();
     }
     if (m <= 64) return launch_gemm<kVarInt8, 64, 64, 8, 3>(w, xq, xs, y, m, s);

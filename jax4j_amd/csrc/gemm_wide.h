@@ -619,3 +619,159 @@ gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs
 
 }  // namespace gw
 }  // namespace j4q
+
+namespace j4q {
+namespace gw {
+
+typedef int32_t i32x4s __attribute__((ext_vector_type(4)));
+
+// Prefill GEMM, int8 variant for small M: the fold of gemm_i8_wide (every output folded by
+// one lane over all blocks in order, bit-identical) on 16 x 16 tiles, so that M = 32 has
+// 512 of them instead of 64 workgroups of 64 x 128. Tile 16 x 32 per workgroup of 2 waves
+// (M = 32, N = 4096: 256 workgroups; M = 128: 1024); wave w owns columns 16 w .. 16 w + 15
+// and all 16 rows, one v_mfma_i32_16x16x32_i8 per block (operand lane (r, g): row r % 16,
+// 8 bytes of k at 8 g). Stages of four blocks (one 128-byte line per row) go through two LDS
+// buffers with the XOR swizzle of gemm_i8_wide; a stage's four MFMAs are issued before
+// their folds. Measured on MI355X (N = K = 4096): M = 32 in 16.8 us, M = 128 in 23.3 us,
+// flat in M up to 64: each wave's 32 stages run back to back at ~0.5 us (neither a deeper
+// load ring nor reading a stage's operands one stage ahead through a third buffer changed
+// that). Requires K % 32 == 0, N % 8 == 0, M * K < 2^31 and N * K < 2^31.
+template <int R>
+__global__ void __launch_bounds__(128)
+gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs, float *__restrict__ y, int M) {
+    static_assert(R % 2 == 0 && R >= 2, "the ring unrolls by an even R");
+    constexpr int BM = 16, BN = 32, SB = 4;  // rows, columns, blocks per stage
+    constexpr int kXS = BM * 128, kWS = BN * 128, kSxS = SB * BM * 4, kDwS = SB * BN * 4;
+    constexpr int kBuf = kXS + kWS + kSxS + kDwS;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBuf];
+    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (nblk + SB - 1) / SB;
+    const int mt = (M + BM - 1) / BM;
+    const int total = (int)gridDim.x;
+    int tile = (int)blockIdx.x;
+    if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+
+    // X: thread t stages 16-byte chunk t % 8 of tile row t / 8; W: chunks t + 128 j.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xq, (uint64_t)M * (uint64_t)K);
+    const int xrow = tid >> 3, xc = tid & 7;
+    const uint32_t xoff = m0 + xrow < M ? (uint32_t)(m0 + xrow) * (uint32_t)K + (uint32_t)xc * 16u : kOob;
+    const int xlds = xrow * 128 + ((xc ^ ((xrow >> 1) & 7)) << 4);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
+    uint32_t woff[2];
+    int wlds[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int q = tid + 128 * j, row = q >> 3, c = q & 7;
+        woff[j] = n0 + row < N ? (uint32_t)(n0 + row) * (uint32_t)K + (uint32_t)c * 16u : kOob;
+        wlds[j] = kXS + row * 128 + ((c ^ ((row >> 1) & 7)) << 4);
+    }
+    // Scales: thread t < 16 loads sx of tile row t (four blocks); thread 16 + u (u < 16)
+    // loads dw of block u / 4 of the stage, columns 8 (u % 4) .. + 7, from the block-major
+    // copy (the block index is a per-lane offset).
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(xs, (uint64_t)M * (uint64_t)nblk * 4u);
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
+    const bool sthr = tid < 16, dthr = tid >= 16 && tid < 32;
+    const int du = tid - 16, dcol = 8 * (du & 3), dblk = du >> 2;
+    const uint32_t soff = sthr && m0 + tid < M ? (uint32_t)(m0 + tid) * (uint32_t)nblk * 4u : kOob;
+    const uint32_t doff = ((uint32_t)(dblk & 3) * (uint32_t)N + (uint32_t)(n0 + dcol)) * 2u;
+
+    struct Set {
+        u32x4 x, w[2], s, d;
+    };
+    Set set[R];
+    auto load = [&](int i, Set &S_) {
+        const bool live = i < ns;
+        const int kb0 = i * SB, k0 = kb0 * 32;
+        S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, live && k0 + xc * 16 < K ? xoff : kOob, (uint32_t)k0, 0));
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int c = (tid + 128 * j) & 7;
+            S_.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live && k0 + c * 16 < K ? woff[j] : kOob, (uint32_t)k0, 0));
+        }
+        const bool dok = dthr && live && kb0 + dblk < nblk && n0 + dcol < N;
+        S_.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, live ? soff : kOob, (uint32_t)kb0 * 4u, 0));
+        S_.d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, dok ? doff : kOob, (uint32_t)kb0 * (uint32_t)N * 2u, 0));
+    };
+    auto store = [&](const Set &S_, int buf) {
+        uint8_t *const b = lds + buf * kBuf;
+        *reinterpret_cast<u32x4 *>(&b[xlds]) = S_.x;
+#pragma unroll
+        for (int j = 0; j < 2; j++) *reinterpret_cast<u32x4 *>(&b[wlds[j]]) = S_.w[j];
+        if (sthr) {
+            float *sx = reinterpret_cast<float *>(b + kXS + kWS) + tid;
+            const f32x4 v = __builtin_bit_cast(f32x4, S_.s);
+            sx[0 * BM] = v.x;
+            sx[1 * BM] = v.y;
+            sx[2 * BM] = v.z;
+            sx[3 * BM] = v.w;
+        } else if (dthr) {
+            float *dw = reinterpret_cast<float *>(b + kXS + kWS + kSxS) + dblk * BN + dcol;
+            // whole-vector casts only (see gemm_i8_wide)
+            const f32x8 f = __builtin_convertvector(__builtin_bit_cast(f16x8, S_.d), f32x8);
+            *reinterpret_cast<f32x4 *>(dw) = __builtin_shufflevector(f, f, 0, 1, 2, 3);
+            *reinterpret_cast<f32x4 *>(dw + 4) = __builtin_shufflevector(f, f, 4, 5, 6, 7);
+        }
+    };
+    // Operand lane (r, g): 8 bytes at k = 8 g of the block, i.e. half g % 2 of 16-byte chunk
+    // 2 kb + g / 2 of the row.
+    const int rb = 16 * wave + r16;
+    const int asw = (r16 >> 1) & 7, bsw = (rb >> 1) & 7;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    auto mfma = [&](const uint8_t *b, int kb) {
+        const int c = 2 * kb + (g >> 1), half = 8 * (g & 1);
+        const long a = *reinterpret_cast<const long *>(&b[r16 * 128 + ((c ^ asw) << 4) + half]);
+        const long q = *reinterpret_cast<const long *>(&b[kXS + rb * 128 + ((c ^ bsw) << 4) + half]);
+        return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, q, i32x4s{0, 0, 0, 0}, 0, 0, 0);
+    };
+    // result element j: row 4 g + j, column lane % 16 of the wave's columns
+    auto fold = [&](const uint8_t *b, int kb, const i32x4s &I) {
+        const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[kb * BN + rb];
+        const f32x4 sx = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(b + kXS + kWS) + kb * BM + 4 * g);
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[j] = __builtin_fmaf((float)I[j], __fmul_rn(sx[j], dw), acc[j]);
+    };
+
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        load(r, set[r]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    store(set[0], 0);
+    // Iteration i: the barrier publishes stage i (stored during iteration i - 1) and frees
+    // the other buffer; the loads of stage i + R go into the set stage i came from; stage
+    // i + 1 is stored while stage i is computed.
+    for (int i0 = 0; i0 < ns; i0 += R) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = i0 + r;  // i0 is a multiple of the even R: buffer i % 2 == r % 2
+            __syncthreads();
+            load(i + R, set[r]);
+            __builtin_amdgcn_sched_barrier(0);
+            store(set[(r + 1) % R], (r + 1) & 1);
+            const uint8_t *b = lds + (r & 1) * kBuf;
+            const int kb0 = i * SB;
+            if (kb0 + SB <= nblk) {
+                i32x4s I[SB];
+#pragma unroll
+                for (int kb = 0; kb < SB; kb++) I[kb] = mfma(b, kb);
+#pragma unroll
+                for (int kb = 0; kb < SB; kb++) fold(b, kb, I[kb]);
+            } else {
+                for (int kb = 0; kb < SB && kb0 + kb < nblk; kb++) fold(b, kb, mfma(b, kb));
+            }
+        }
+    }
+    const int col = n0 + rb;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int row = m0 + 4 * g + j;
+        if (row < M && col < N) y[(int64_t)row * N + col] = acc[j];
+    }
+}
+
+}  // namespace gw
+}  // namespace j4q

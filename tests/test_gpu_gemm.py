@@ -29,8 +29,9 @@ TOL_ACCUM = 2e-5  # fp32 accumulation-order difference only
 # (M, N, K): tails in every dimension, one K block, the benchmark K, M above one tile. The
 # bf16 variant runs M <= 32 and 33..128 on the small-M kernel (16 weight rows per workgroup,
 # stages of 512 or 256 k: K = 32, 256 and 4096 cover a partial first stage, one stage and
-# many), 129..511 on the older 4-wave kernel. The int8 variant runs M <= 64 (and N % 8 != 0)
-# on the older 4-wave kernel, the rest on the 8-wave one.
+# many), 129..511 on the older 4-wave kernel. The int8 variant runs N % 8 == 0 on the
+# 2-wave 16 x 32 tile kernel up to M = 256 and the 8-wave 64 x 128 one above; N % 8 != 0
+# (257 here) on the older 4-wave kernel.
 SHAPES = [(1, 32, 32), (5, 13, 256), (33, 96, 512), (128, 128, 128), (130, 257, 1024), (64, 384, 4096),
           (32, 200, 4096), (100, 48, 800)]
 
@@ -99,10 +100,12 @@ def test_gemm_bf16_matches_reference(backend, m, n, k):
         backend.release(h)
 
 
-# The int8 variant runs M > 64 with N % 8 == 0 on the 8-wave 64 x 128 tile kernel (stages
-# of four blocks): one block; a partial last stage (K = 96, 160, 800); tails in M and N; the
-# benchmark K. Every case is bit-identical to the emulation, which folds blocks in order.
-INT8_WIDE_SHAPES = [(65, 8, 32), (512, 136, 96), (600, 1024, 4096), (2048, 256, 160), (100, 48, 800)]
+# The int8 kernels with N % 8 == 0 (stages of four blocks): one block; a partial last stage
+# (K = 96, 160, 800); tails in M and N; the benchmark K; both sides of the M = 256 switch
+# between the 16 x 32 and 64 x 128 tile kernels. Every case is bit-identical to the
+# emulation, which folds blocks in order.
+INT8_WIDE_SHAPES = [(65, 8, 32), (512, 136, 96), (600, 1024, 4096), (2048, 256, 160), (100, 48, 800),
+                    (7, 40, 4096), (256, 64, 1024), (257, 64, 1024), (30, 1000, 2080)]
 
 
 @pytest.mark.parametrize("m,n,k", INT8_WIDE_SHAPES)
