@@ -436,9 +436,10 @@ hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64
         else gw::gemm_bf16_wide<128, 1, 4><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
         return hipGetLastError();
     }
-    if (m <= 128 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
+    if (m <= 192 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
         // gemm_wide.h, small M: 16 weight rows per workgroup, all of K (measured on MI355X,
-        // N = K = 4096: M = 32 in 11.7 us, M = 128 in 23.0 us with 64-row tiles)
+        // N = K = 4096: M = 32 in 11.7 us, M = 128 in 23.0 us with 64-row tiles, M = 192 in
+        // 31.6 us against 34.1 on the 4-wave kernel; 128-row tiles are no faster at M = 128)
         const int64_t nt = (w.rows + 15) / 16, bm = m <= 32 ? 32 : 64;
         const int64_t grid = ((m + bm - 1) / bm) * nt;
         if (grid > 0x7fffffff) return hipErrorInvalidValue;

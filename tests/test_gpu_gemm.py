@@ -27,13 +27,13 @@ TOL_BF16X = 1e-2  # bf16-activation configs
 TOL_ACCUM = 2e-5  # fp32 accumulation-order difference only
 
 # (M, N, K): tails in every dimension, one K block, the benchmark K, M above one tile. The
-# bf16 variant runs M <= 32 and 33..128 on the small-M kernel (16 weight rows per workgroup,
+# bf16 variant runs M <= 32 and 33..192 on the small-M kernel (16 weight rows per workgroup,
 # stages of 512 or 256 k: K = 32, 256 and 4096 cover a partial first stage, one stage and
-# many), 129..511 on the older 4-wave kernel. The int8 variant runs N % 8 == 0 on the
+# many), 193..511 on the older 4-wave kernel. The int8 variant runs N % 8 == 0 on the
 # 2-wave 16 x 32 tile kernel up to M = 256 and the 8-wave 64 x 128 one above; N % 8 != 0
 # (257 here) on the older 4-wave kernel.
 SHAPES = [(1, 32, 32), (5, 13, 256), (33, 96, 512), (128, 128, 128), (130, 257, 1024), (64, 384, 4096),
-          (32, 200, 4096), (100, 48, 800)]
+          (32, 200, 4096), (100, 48, 800), (192, 96, 512), (200, 64, 256)]
 
 
 def note(*parts):
