@@ -198,7 +198,7 @@ BATCH_CASES = [
 
 
 @pytest.mark.parametrize("qt,rows,cols", BATCH_CASES, ids=lambda v: getattr(v, "name", str(v)))
-@pytest.mark.parametrize("B", [3, 8, 9, 16])
+@pytest.mark.parametrize("B", [3, 8, 9, 16, 21])
 def test_gemv_batched_matches_oracle(backend, uploaded, qt, rows, cols, B):
     note("batched", qt.name, rows, cols, "B", B)
     blob, w = uploaded(qt, rows, cols)
@@ -272,9 +272,12 @@ def test_gemv_batched_wide_k(backend, uploaded, qt, rows, cols, B):
 
 
 @pytest.mark.parametrize("cols", [4096, 11008])
-def test_gemv_batched_add_in_place(backend, uploaded, cols):
-    """quantMatvecAdd with y on the add buffer itself (a residual updated in place)."""
-    qt, rows, B = QuantType.Q4_0, 1000, 8
+@pytest.mark.parametrize("B", [8, 16])
+def test_gemv_batched_add_in_place(backend, uploaded, cols, B):
+    """quantMatvecAdd with y on the add buffer itself (a residual updated in place). With 16
+    rows and K > 2048 the in-place call runs two 8-row launches of one window each, the
+    out-of-place one a 16-row launch in 2048-column windows."""
+    qt, rows = QuantType.Q4_0, 1000
     note("batched in-place add", qt.name, rows, cols, "B", B)
     blob, w = uploaded(qt, rows, cols)
     xs = S.activations_f32(rows + 3, B * cols).reshape(B, cols)
@@ -287,7 +290,7 @@ def test_gemv_batched_add_in_place(backend, uploaded, cols):
     backend.quant_matvec_into(w, backend.buffer_desc(xb).device_ptr, rp, rp, B)
     backend.sync()
     got = backend.download(res).reshape(B, rows)
-    if cols <= 4096:  # one window: the same kernel as the out-of-place call
+    if cols <= 4096 and B <= 8:  # one window: the same kernel as the out-of-place call
         assert np.array_equal(bits(got), bits(ref))
     for b in range(B):
         y64 = oracle.matvec_f64(qt.id, blob, rows, cols, xs[b]) + add[b].astype(np.float64)
