@@ -429,11 +429,19 @@ hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64
     if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols * 2 > 0x7fffffffull) return hipErrorInvalidValue;
     if (m >= 512 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
         // gemm_wide.h: 128 x 128 tiles when they fill the GPU, else 128 x 64 (measured on
-        // MI355X, M = 512: 38.3 us against 39.7 us for 64 x 128 tiles)
+        // MI355X, M = 512: 38.3 us against 39.7 us for 64 x 128 tiles). Even N takes the
+        // kernel that loads its tiles straight into LDS (bit-identical; M = 512: 29-31 us
+        // against 36.6, M = 2048: 79-89 against 106.6, same box).
         const int64_t mt = (m + 127) / 128, t128 = mt * ((w.rows + 127) / 128), t64 = mt * ((w.rows + 63) / 64);
         if (t64 > 0x7fffffff) return hipErrorInvalidValue;
-        if (t128 >= 256) gw::gemm_bf16_wide<128, 2, 4><<<(unsigned)t128, 512, 0, s>>>(w, x, y, (int)m);
-        else gw::gemm_bf16_wide<128, 1, 4><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
+        if (w.rows % 2 == 0) {
+            if (t128 >= 256) gw::gemm_bf16_lds<128, 2, true><<<(unsigned)t128, 512, 0, s>>>(w, x, y, (int)m);
+            else gw::gemm_bf16_lds<128, 1, false><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
+        } else if (t128 >= 256) {
+            gw::gemm_bf16_wide<128, 2, 4><<<(unsigned)t128, 512, 0, s>>>(w, x, y, (int)m);
+        } else {
+            gw::gemm_bf16_wide<128, 1, 4><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
+        }
         return hipGetLastError();
     }
     if (m <= 192 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {

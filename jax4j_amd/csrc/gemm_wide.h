@@ -265,6 +265,230 @@ gemm_bf16_wide(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, in
             }
 }
 
+// ---- The same product with the tiles loaded straight into LDS ----------------------------
+//
+// buffer_load_dwordx4 ... lds writes a wave's 64 x 16 bytes to LDS at M0 + 16 lane without
+// passing through VGPRs (lane layout and zero fill of out-of-range lanes checked on MI355X).
+// The host pass of hipcc checks the builtin's 16-byte size against the host target and
+// rejects it, so the call exists in the device pass only.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t vo, uint32_t so) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, vo, so, 0, 0);
+#endif
+}
+
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t vo) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4, vo, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+// A workgroup barrier without __syncthreads()'s release fence: the fence would wait for every
+// LDS load in flight (vmcnt(0)), which is the ring this kernel keeps open. The empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Prefill GEMM, bf16 variant for M >= 512 and even N, results bit-identical to
+// gemm_bf16_wide (the same blocks go to the same waves in the same order):
+//  - Tile BM x 64 NJ per workgroup of 8 waves; wave w owns columns [16 NJ (w % 4), +16 NJ)
+//    and blocks 2 b + w / 4 (b = 0, 1) of every 128-k stage, for all BM rows.
+//  - Every stage moves straight from global memory into one of three LDS stage buffers:
+//    X as BM rows x 256 bytes (16-byte chunk c of row r at c ^ (r % 16): the 16 rows of an
+//    operand read fall on distinct banks), W as BN rows x 128 bytes (chunk c of row r at
+//    c ^ ((r / 2) % 8)), and each wave's scales of the stage into its own 256-byte slot.
+//    Each wave's LDS loads pick the global chunk that belongs at their lane's LDS slot.
+//  - The buffers are separate __shared__ arrays and the ring is unrolled by three, so the
+//    compiler knows which loads write the buffer a read touches and adds no waits of its
+//    own; the kernel waits for its stage with vmcnt(loads of one stage) and a barrier.
+//  - Iteration i: wait for own stage-i loads and LDS reads, barrier (stage i is in LDS for
+//    every wave, every read of stage i - 1 is done), load stage i + 2 into the buffers of
+//    stage i - 1, read all operands of stage i, dequantize W and run the MFMAs. With ILV
+//    the stage i + 2 loads are spread between the MFMAs (measured faster at 128 x 128
+//    tiles: a wave blocks while the load path accepts its loads); otherwise they go first.
+//  - Stages past the end load zeros (out-of-range offsets) and add exact zeros; all LDS
+//    loads have landed (vmcnt(0)) before the partial tiles reuse the X buffers.
+// grid = ceil(M / BM) * ceil(N / (64 NJ)) workgroups of 512 threads. Requires N even,
+// K % 32 == 0, M * K * 2 < 2^31, N * K < 2^31 and the block-major scale copy in w.d.
+template <int BM, int NJ, bool ILV>
+__global__ void __launch_bounds__(512)
+gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M) {
+    static_assert(BM == 64 || BM == 128, "64 or 128 rows");
+    constexpr int BN = 64 * NJ, TM = BM / 16, XD = BM / 32;  // X loads per wave and stage
+    constexpr int kX = BM * 256, kW = BN * 128;
+    constexpr int P = XD + NJ + 1;  // vector-memory instructions per wave and stage
+    __shared__ __attribute__((aligned(1024))) uint8_t xs0[kX], xs1[kX], xs2[kX];
+    __shared__ __attribute__((aligned(1024))) uint8_t ws0[kW], ws1[kW], ws2[kW];
+    __shared__ __attribute__((aligned(1024))) uint8_t ds0[2048], ds1[2048], ds2[2048];
+    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (K + 127) / 128;
+    const int mt = (M + BM - 1) / BM;
+    // Workgroup b runs on XCD b % 8; tile order is m fastest and each XCD takes a contiguous
+    // range of it, so the m tiles of a group of n tiles (the same W rows) share an L2.
+    const int total = (int)gridDim.x;
+    int tile = (int)blockIdx.x;
+    if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nw = wave & 3, kh = wave >> 2;  // column group, block parity
+    const int m16 = lane & 15, g = lane >> 4;
+
+    // X load j of this wave covers rows 4 (8 j + wave) .. +3; lane L fills LDS slot L % 16 of
+    // row 4 (8 j + wave) + L / 16, which holds chunk (L % 16) ^ (row % 16).
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint64_t)M * (uint64_t)K * 2u);
+    uint32_t xoff[XD];
+    int xk[XD];
+#pragma unroll
+    for (int j = 0; j < XD; j++) {
+        const int row = 4 * (8 * j + wave) + (lane >> 4), c = (lane & 15) ^ (row & 15), gm = m0 + row;
+        xoff[j] = gm < M ? (uint32_t)gm * (uint32_t)K * 2u + (uint32_t)c * 16u : kOob;
+        xk[j] = c * 8;
+    }
+    // W load j covers rows 8 (8 j + wave) .. +7; slot L % 8 of row 8 (8 j + wave) + L / 8
+    // holds chunk (L % 8) ^ ((row / 2) % 8).
+    const __amdgpu_buffer_rsrc_t wq = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
+    uint32_t woff[NJ];
+    int wk[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int row = 8 * (8 * j + wave) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7), n = n0 + row;
+        woff[j] = n < N ? (uint32_t)n * (uint32_t)K + (uint32_t)c * 16u : kOob;
+        wk[j] = c * 16;
+    }
+    // Scales, 4 bytes per lane: lane L < 16 NJ loads the scales of rows r + 2 (L % 8 NJ) and
+    // r + 2 (L % 8 NJ) + 1 (r = the wave's first column) for block 2 (L / 8 NJ) + kh of the
+    // stage; the slot is [2 blocks][16 NJ rows] fp16 (N even keeps both rows in range).
+    const __amdgpu_buffer_rsrc_t wd = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
+    const int dbb = lane / (8 * NJ), drow = n0 + 16 * NJ * nw + 2 * (lane % (8 * NJ));
+    const bool dlane = lane < 16 * NJ && drow < N;
+    const uint32_t doff = (uint32_t)drow * 2u;
+
+    // Load p (0 <= p < P) of this wave for stage i.
+    auto load = [&](int i, int p, uint8_t *xb, uint8_t *wb, uint8_t *db) {
+        const int k0 = i * 128;
+        const bool live = i < ns;
+        if (p < XD) {
+            const bool ok = live && k0 + xk[p] < K;
+            dma16(xr, xb + (8 * p + wave) * 1024, ok ? xoff[p] : kOob, (uint32_t)k0 * 2u);
+        } else if (p < XD + NJ) {
+            const int j = p - XD;
+            const bool ok = live && k0 + wk[j] < K;
+            dma16(wq, wb + (8 * j + wave) * 1024, ok ? woff[j] : kOob, (uint32_t)k0);
+        } else {
+            const int kb = 4 * i + 2 * dbb + kh;
+            const bool ok = live && dlane && kb < nblk;
+            dma4(wd, db + wave * 256, ok ? doff + (uint32_t)kb * (uint32_t)N * 2u : kOob);
+        }
+    };
+
+    f32x4 acc[TM][NJ];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Stage in (xb, wb, db) and the loads of stage inext into (xn, wn, dn).
+    // A operand of row tile t, block b: row 16 t + m16, chunk 4 (2 b + kh) + g, at slot
+    // chunk ^ m16. B operand of column tile j: row 16 NJ nw + 16 j + m16, bytes
+    // 32 (2 b + kh) + 8 g, i.e. chunk 2 (2 b + kh) + g / 2 at slot chunk ^ ((row / 2) % 8),
+    // half g % 2.
+    auto stage = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *db, int inext, uint8_t *xn, uint8_t *wn,
+                     uint8_t *dn) {
+        if (!ILV) {
+#pragma unroll
+            for (int p = 0; p < P; p++) load(inext, p, xn, wn, dn);
+        }
+        bf16x8 a[2][TM], b[2][NJ];
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            const int ca = 4 * (2 * bb + kh) + g;
+            const int aoff = m16 * 256 + ((ca ^ m16) << 4);
+#pragma unroll
+            for (int t = 0; t < TM; t++) a[bb][t] = *reinterpret_cast<const bf16x8 *>(xb + t * 16 * 256 + aoff);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int row = 16 * NJ * nw + 16 * j + m16, cb = 2 * (2 * bb + kh) + (g >> 1);
+                const u32x2 q = *reinterpret_cast<const u32x2 *>(wb + row * 128 + ((cb ^ ((row >> 1) & 7)) << 4) + 8 * (g & 1));
+                const uint32_t dbits = *reinterpret_cast<const uint16_t *>(db + wave * 256 + (bb * 16 * NJ + 16 * j + m16) * 2);
+                b[bb][j] = dequant8(q, half_bits_to_float(dbits));
+            }
+        }
+        constexpr int NM = 2 * TM * NJ, STRIDE = NM / P > 0 ? NM / P : 1;
+        int mi = 0, p = 0;
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+            for (int t = 0; t < TM; t++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[bb][t], b[bb][j], acc[t][j], 0, 0, 0);
+                    if (ILV && mi % STRIDE == STRIDE - 1 && p < P) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        load(inext, p, xn, wn, dn);
+                        __builtin_amdgcn_sched_barrier(0);
+                        p++;
+                    }
+                    mi++;
+                }
+        if (ILV) {
+#pragma unroll
+            for (; p < P; p++) load(inext, p, xn, wn, dn);
+        }
+    };
+
+#pragma unroll
+    for (int p = 0; p < P; p++) load(0, p, xs0, ws0, ds0);
+#pragma unroll
+    for (int p = 0; p < P; p++) load(1, p, xs1, ws1, ds1);
+    for (int i0 = 0; i0 < ns; i0 += 3) {
+        wait_vm_lgkm0<P>();
+        lds_barrier();
+        stage(xs0, ws0, ds0, i0 + 2, xs2, ws2, ds2);
+        wait_vm_lgkm0<P>();
+        lds_barrier();
+        stage(xs1, ws1, ds1, i0 + 3, xs0, ws0, ds0);
+        wait_vm_lgkm0<P>();
+        lds_barrier();
+        stage(xs2, ws2, ds2, i0 + 4, xs1, ws1, ds1);
+    }
+
+    // ---- epilogue: the odd-block waves hand their partial tiles to the even-block waves,
+    // which add them (even + odd) and store. Result element v of tile (t, j) is row
+    // 16 t + 4 g + v, column 16 j + lane % 16 of the wave's columns.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(nw < 2 ? xs0 : xs1);
+    if (kh == 1) {
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) red[((((nw & 1) * TM + t) * NJ + j) * 4 + v) * 64 + lane] = acc[t][j][v];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int row = m0 + 16 * t + 4 * g + v, col = n0 + 16 * NJ * nw + 16 * j + m16;
+                const float s = acc[t][j][v] + red[((((nw & 1) * TM + t) * NJ + j) * 4 + v) * 64 + lane];
+                if (row < M && col < N) y[(int64_t)row * N + col] = s;
+            }
+}
+
 }  // namespace gw
 }  // namespace j4q
 

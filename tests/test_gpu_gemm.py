@@ -122,7 +122,11 @@ def test_gemm_int8_wide_tiles_bit_exact(backend, m, n, k):
 
 # M >= 512 runs the wide-tile kernel: 128 x 64 tiles while 128 x 128 ones would be fewer
 # than 256 (one stage; a half stage at the end; tails in M and N), 128 x 128 from 256 tiles.
-WIDE_SHAPES = [(512, 128, 64), (600, 200, 96), (640, 520, 2048), (2048, 2048, 128)]
+# The bf16 variant at M >= 512 loads its tiles straight into LDS for even N (128 x 64 tiles,
+# or 128 x 128 once those fill the GPU: (2048, 2048) and (1030, 4098)) and runs the older
+# register-staged kernel for odd N (129, 2049). K = 64, 96 and 160 end in a partial stage.
+WIDE_SHAPES = [(512, 128, 64), (600, 200, 96), (640, 520, 2048), (2048, 2048, 128), (1030, 4098, 160),
+               (512, 129, 256), (2048, 2049, 64)]
 
 
 @pytest.mark.parametrize("m,n,k", WIDE_SHAPES)
@@ -139,6 +143,27 @@ def test_gemm_bf16_wide_tiles(backend, m, n, k):
         assert np.array_equal(bits(backend.download(y2).reshape(m, n)), bits(got))
         backend.release(y2)
     for h in (w, x, y):
+        backend.release(h)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 128, 256), (2048, 2048, 128)])
+def test_gemm_bf16_lds_kernel_matches_register_staged(backend, m, n, k):
+    """The two M >= 512 bf16 kernels give every block to the same wave in the same order, so
+    the first n columns of an (n + 1)-row matrix (odd: register-staged kernel) equal the
+    n-row matrix's (even: LDS-loading kernel) bit for bit."""
+    note("gemm bf16 lds vs wide", m, n, k)
+    w_blob = S.quant_blocks(QuantType.Q8_0, 5000 + m + n, n + 1, k)
+    xb = S.activations_bf16(5001 + m, m * k).reshape(m, k)
+    x = backend.upload(xb, shape=(m, k), dtype=DType.BF16)
+    w_odd = backend.upload_quantized(w_blob, QuantType.Q8_0, (n + 1, k))
+    head = np.ascontiguousarray(np.frombuffer(bytes(w_blob), dtype=np.uint8)[: n * (k // 32) * 34])
+    w_even = backend.upload_quantized(head, QuantType.Q8_0, (n, k))
+    y_odd = backend.quant_matmul(w_odd, x, "bf16")
+    y_even = backend.quant_matmul(w_even, x, "bf16")
+    a = backend.download(y_odd).reshape(m, n + 1)[:, :n]
+    b = backend.download(y_even).reshape(m, n)
+    assert np.array_equal(bits(a), bits(b))
+    for h in (x, w_odd, w_even, y_odd, y_even):
         backend.release(h)
 
 
