@@ -427,21 +427,35 @@ hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs,
 hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s) {
     if (m <= 0 || w.rows <= 0) return hipSuccess;
     if (m > 65535 * 64 || w.cols % 32 != 0 || (uint64_t)m * w.cols * 2 > 0x7fffffffull) return hipErrorInvalidValue;
+    if (m > 64 && w.rows % 2 == 0 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
+        // gemm_wide.h, tiles loaded straight into LDS: the largest tile whose grid still
+        // fills the GPU (measured on MI355X, K = 4096: M = 512, N = 4096 in 29-30 us at
+        // 128 x 64; M = 2048 in 90 us at 128 x 128; M = 128..256, N = 4096 in 18.5-19.9 us at
+        // 64 x 64, against 20.8-36.4 us on the small-M and 4-wave kernels; with fewer than 128
+        // workgroups those kernels are faster: M = 64, or N = 1024 at M = 128)
+        const int64_t nt64 = (w.rows + 63) / 64, nt128 = (w.rows + 127) / 128;
+        const int64_t g128x128 = ((m + 127) / 128) * nt128, g128 = ((m + 127) / 128) * nt64, g64 = ((m + 63) / 64) * nt64;
+        if (g64 > 0x7fffffff) return hipErrorInvalidValue;
+        if (g128x128 >= 256) {
+            gw::gemm_bf16_lds<128, 2, true><<<(unsigned)g128x128, 512, 0, s>>>(w, x, y, (int)m);
+            return hipGetLastError();
+        }
+        if (g128 >= 192) {
+            gw::gemm_bf16_lds<128, 1, false><<<(unsigned)g128, 512, 0, s>>>(w, x, y, (int)m);
+            return hipGetLastError();
+        }
+        if (g64 >= 128) {
+            gw::gemm_bf16_lds<64, 1, false><<<(unsigned)g64, 512, 0, s>>>(w, x, y, (int)m);
+            return hipGetLastError();
+        }
+    }
     if (m >= 512 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {
-        // gemm_wide.h: 128 x 128 tiles when they fill the GPU, else 128 x 64 (measured on
-        // MI355X, M = 512: 38.3 us against 39.7 us for 64 x 128 tiles). Even N takes the
-        // kernel that loads its tiles straight into LDS (bit-identical; M = 512: 29-31 us
-        // against 36.6, M = 2048: 79-89 against 106.6, same box).
+        // gemm_wide.h, register-staged (odd N, or too few tiles for the kernel above): 128 x 128
+        // tiles when they fill the GPU, else 128 x 64
         const int64_t mt = (m + 127) / 128, t128 = mt * ((w.rows + 127) / 128), t64 = mt * ((w.rows + 63) / 64);
         if (t64 > 0x7fffffff) return hipErrorInvalidValue;
-        if (w.rows % 2 == 0) {
-            if (t128 >= 256) gw::gemm_bf16_lds<128, 2, true><<<(unsigned)t128, 512, 0, s>>>(w, x, y, (int)m);
-            else gw::gemm_bf16_lds<128, 1, false><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
-        } else if (t128 >= 256) {
-            gw::gemm_bf16_wide<128, 2, 4><<<(unsigned)t128, 512, 0, s>>>(w, x, y, (int)m);
-        } else {
-            gw::gemm_bf16_wide<128, 1, 4><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
-        }
+        if (t128 >= 256) gw::gemm_bf16_wide<128, 2, 4><<<(unsigned)t128, 512, 0, s>>>(w, x, y, (int)m);
+        else gw::gemm_bf16_wide<128, 1, 4><<<(unsigned)t64, 512, 0, s>>>(w, x, y, (int)m);
         return hipGetLastError();
     }
     if (m <= 192 && (uint64_t)w.rows * w.cols <= 0x7fffffffull) {

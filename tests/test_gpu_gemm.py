@@ -29,7 +29,8 @@ TOL_ACCUM = 2e-5  # fp32 accumulation-order difference only
 # (M, N, K): tails in every dimension, one K block, the benchmark K, M above one tile. The
 # bf16 variant runs M <= 32 and 33..192 on the small-M kernel (16 weight rows per workgroup,
 # stages of 512 or 256 k: K = 32, 256 and 4096 cover a partial first stage, one stage and
-# many), 193..511 on the older 4-wave kernel. The int8 variant runs N % 8 == 0 on the
+# many) and 193..511 on the older 4-wave kernel when the grid is too small for the kernels
+# that load their tiles straight into LDS (WIDE_SHAPES below cover those). The int8 variant runs N % 8 == 0 on the
 # 2-wave 16 x 32 tile kernel up to M = 256 and the 8-wave 64 x 128 one above; N % 8 != 0
 # (257 here) on the older 4-wave kernel.
 SHAPES = [(1, 32, 32), (5, 13, 256), (33, 96, 512), (128, 128, 128), (130, 257, 1024), (64, 384, 4096),
@@ -122,11 +123,13 @@ def test_gemm_int8_wide_tiles_bit_exact(backend, m, n, k):
 
 # M >= 512 runs the wide-tile kernel: 128 x 64 tiles while 128 x 128 ones would be fewer
 # than 256 (one stage; a half stage at the end; tails in M and N), 128 x 128 from 256 tiles.
-# The bf16 variant at M >= 512 loads its tiles straight into LDS for even N (128 x 64 tiles,
-# or 128 x 128 once those fill the GPU: (2048, 2048) and (1030, 4098)) and runs the older
-# register-staged kernel for odd N (129, 2049). K = 64, 96 and 160 end in a partial stage.
+# The bf16 variant above M = 64 with even N loads its tiles straight into LDS when the grid
+# is large enough: 128 x 128 tiles from 256 of them ((2048, 2048), (1030, 4098)), else
+# 128 x 64 from 192 ((384, 4096)), else 64 x 64 from 128 ((96, 4096), (200, 2048)); smaller
+# grids ((512, 128), (600, 200), (640, 520)) and odd N ((512, 129), (2048, 2049)) run the
+# register-staged kernel at M >= 512. K = 64, 96 and 160 end in a partial stage.
 WIDE_SHAPES = [(512, 128, 64), (600, 200, 96), (640, 520, 2048), (2048, 2048, 128), (1030, 4098, 160),
-               (512, 129, 256), (2048, 2049, 64)]
+               (512, 129, 256), (2048, 2049, 64), (384, 4096, 128), (96, 4096, 160), (200, 2048, 96)]
 
 
 @pytest.mark.parametrize("m,n,k", WIDE_SHAPES)
