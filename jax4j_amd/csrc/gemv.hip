@@ -29,22 +29,29 @@ int g_cus = 256;
 // Items per wave of launch_mfma: 8 waves x items x blocks per item is the launch window,
 // 128 blocks (4096 columns) for up to 8 batch rows; 64 blocks at 16 rows, whose x image of
 // 16 rows x 4096 columns would not fit in LDS.
+// Waves per workgroup: 16 for Q8_0 and Q4_0 up to 8 rows (half the items per wave, twice the
+// waves to hide the load latency: Q8_0 4096 x 4096 at B = 8 12.8 -> 10.9 us, Q4_0 11008 x
+// 4096 12.4 -> 12.0 us; Q4_K was 2 % slower and Q6_K spilled registers), else 8. The window
+// (waves x items x blocks per item) is the same either way.
 template <int FMT, int BB>
-constexpr int mfma_ipw() { return (FMT == Q8_0 ? 8 : 4) / (BB > 8 ? 2 : 1); }
+constexpr int mfma_waves() { return BB <= 8 && (FMT == Q8_0 || FMT == Q4_0) ? 16 : 8; }
 template <int FMT, int BB>
-constexpr int mfma_window() { return 8 * mfma_ipw<FMT, BB>() * (FMT == Q8_0 ? 2 : 4); }
+constexpr int mfma_ipw() { return (FMT == Q8_0 ? 8 : 4) / (BB > 8 ? 2 : 1) * 8 / mfma_waves<FMT, BB>(); }
+template <int FMT, int BB>
+constexpr int mfma_window() { return mfma_waves<FMT, BB>() * mfma_ipw<FMT, BB>() * (FMT == Q8_0 ? 2 : 4); }
 
 // Batched GEMV on the matrix cores (gemv_mfma.h) for up to 16 batch rows per launch:
-// persistent grid of one 8-wave workgroup per CU, each launch a window of up to 128 blocks
-// (4096 columns; 64 at 16 rows) split into 8 wave slices; a wider K runs as equal windows,
+// persistent grid of one workgroup per CU, each launch a window of up to 128 blocks (4096
+// columns; 64 at 16 rows) split into one slice per wave; a wider K runs as equal windows,
 // each adding the previous window's output. Measured on MI355X (Q4_0 11008 x 4096): B = 4
 // 10.8 us, B = 8 12.4 us, against 22 us and 41 us for one vector-ALU pass per batch row;
 // at B <= 2 the two are level. The Llama-3-8B decode step at B = 16 takes 4.8 ms with one
 // 16-row pass per matrix, 6.1 ms with two 8-row passes.
 template <int FMT, int BB>
 hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
-    constexpr int IPW = mfma_ipw<FMT, BB>(), S = FMT == Q8_0 ? 2 : 4, CAP = mfma_window<FMT, BB>();
-    static_assert(CAP == 8 * IPW * S, "window = waves x items per wave x tile sets");
+    constexpr int W = mfma_waves<FMT, BB>(), IPW = mfma_ipw<FMT, BB>(), S = FMT == Q8_0 ? 2 : 4;
+    constexpr int CAP = mfma_window<FMT, BB>();
+    static_assert(CAP == W * IPW * S && CAP == (BB > 8 ? 64 : 128), "window = waves x items per wave x blocks per item");
     const int tiles = (int)((m.rows + 15) / 16);
     const int grid = tiles < g_cus ? tiles : g_cus;
     const int nb = (int)(m.cols / 32);
@@ -57,7 +64,7 @@ hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y
     for (int kb0 = 0; kb0 < nb; kb0 += per) {
         const int kbn = nb - kb0 < per ? nb - kb0 : per;
         const bool last = kb0 + kbn >= nb;
-        const hipError_t e = gmf::launch_k<FMT, BB, 8, IPW, false, 2>(m, x, last ? add : nullptr, y, b, grid, s, kb0, kbn,
+        const hipError_t e = gmf::launch_k<FMT, BB, W, IPW, false, 2>(m, x, last ? add : nullptr, y, b, grid, s, kb0, kbn,
                                                                         kb0 == 0 ? nullptr : y);
         if (e != hipSuccess) return e;
     }

@@ -170,9 +170,9 @@ struct Plan {
     static constexpr int kBytes = kPa + RT * BB * 16 * 8;
 };
 
-// Tiles per round (one pair of barriers per round): 4, or 2 at BB = 16 (LDS).
-template <int BB>
-constexpr int round_tiles() { return BB <= 8 ? 4 : 2; }
+// Tiles per round (one pair of barriers per round): 4, or 2 at BB = 16 or 16 waves (LDS).
+template <int BB, int WAVES>
+constexpr int round_tiles() { return BB <= 8 && WAVES <= 8 ? 4 : 2; }
 
 // grid: G_wg persistent workgroups of WAVES waves; workgroup w takes 16-row tiles w,
 // w + G_wg, ... The kernel covers the window of blocks [kb0, kb0 + kbn) of every row:
@@ -192,7 +192,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     constexpr int S = F::S, G = F::GROUPS, NBW = IPW * S;
     constexpr bool W16 = BB == 16;  // two A operands (hi, lo) of 16 batch rows each
     static_assert(BB <= 8 || (W16 && !XREG), "BB up to 8, or 16 without XREG");
-    constexpr int RT = round_tiles<BB>();
+    constexpr int RT = round_tiles<BB, WAVES>();
     static_assert(RT % TS == 0, "a round holds whole turns of the tile ring");
     using P = Plan<BB, G, WAVES, NBW, RT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -634,7 +634,7 @@ hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, i
                     int kb0 = 0, int kbn = -1, const float *prev = nullptr) {
     if (kbn < 0) kbn = (int)(m.cols / 32);
     constexpr int NBW = IPW * Fmt<FMT>::S;
-    constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW, round_tiles<BB>()>::kBytes;
+    constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW, round_tiles<BB, WAVES>()>::kBytes;
     static_assert(lds <= 160 * 1024, "LDS of one workgroup");
     gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<grid, WAVES * 64, lds, s>>>(m, x, prev, add, y, B, kb0, kbn);
     return hipGetLastError();
