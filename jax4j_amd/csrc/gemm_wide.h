@@ -849,35 +849,47 @@ namespace gw {
 
 typedef int32_t i32x4s __attribute__((ext_vector_type(4)));
 
-// Prefill GEMM, int8 variant for small M: the fold of gemm_i8_wide (every output folded by
-// one lane over all blocks in order, bit-identical) on 16 x 16 tiles, so that M = 32 has
-// 512 of them instead of 64 workgroups of 64 x 128. Tile 16 x 32 per workgroup of 2 waves
-// (M = 32, N = 4096: 256 workgroups; M = 128: 1024); wave w owns columns 16 w .. 16 w + 15
-// and all 16 rows, one v_mfma_i32_16x16x32_i8 per block (operand lane (r, g): row r % 16,
-// 8 bytes of k at 8 g). Stages of four blocks (one 128-byte line per row) go through two LDS
-// buffers with the XOR swizzle of gemm_i8_wide; a stage's four MFMAs are issued before
-// their folds. Measured on MI355X (N = K = 4096): M = 32 in 16.8 us, M = 128 in 23.3 us,
-// flat in M up to 64: each wave's 32 stages run back to back at ~0.5 us (neither a deeper
-// load ring nor reading a stage's operands one stage ahead through a third buffer changed
-// that). Requires K % 32 == 0, N % 8 == 0, M * K < 2^31 and N * K < 2^31.
-template <int R>
-__global__ void __launch_bounds__(128)
+// Prefill GEMM, int8 variant for small M: the fold of gemm_i8_wide on 16 x 32 tiles, with K
+// cut into RG = 1 or 4 contiguous ranges of whole stages, each run by its own pair of waves
+// through its own LDS buffers. With one lane per output over all of K, M = 32 would have only
+// 512 16 x 16 tiles (two waves per CU) whose 32 stages run back to back; four ranges give
+// eight waves per workgroup and a quarter of the stages each (used while the tiles do not
+// exceed the CUs; with more tiles the single range is faster: M = 128 27.4 us against 42.6). Wave (p, h) = (w / 2, w % 2) owns
+// columns 16 h .. 16 h + 15 and range p (stages [p L, (p + 1) L), L = ceil(stages / 4)), one
+// v_mfma_i32_16x16x32_i8 per block (operand lane (r, g): row r % 16, 8 bytes of k at 8 g),
+// folded in block order into its partial; the partials meet at the end as
+// ((p0 + p1) + p2) + p3, the association of the oracle's emulation with four ranges.
+// Stages of four blocks (one 128-byte line per row) go through two LDS buffers per range
+// with the XOR swizzle of gemm_i8_wide; a stage's four MFMAs are issued before their folds.
+// Every range runs the same number of iterations (its stages past its range load nothing
+// and compute nothing), so all waves meet at every barrier. Requires K % 32 == 0,
+// N % 8 == 0, M * K < 2^31 and N * K < 2^31.
+template <int R, int RG>
+__global__ void __launch_bounds__(128 * RG)
 gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs, float *__restrict__ y, int M) {
     static_assert(R % 2 == 0 && R >= 2, "the ring unrolls by an even R");
     constexpr int BM = 16, BN = 32, SB = 4;  // rows, columns, blocks per stage
     constexpr int kXS = BM * 128, kWS = BN * 128, kSxS = SB * BM * 4, kDwS = SB * BN * 4;
     constexpr int kBuf = kXS + kWS + kSxS + kDwS;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBuf];
-    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (nblk + SB - 1) / SB;
+    static_assert(RG == 1 || RG == 4, "one or four K ranges");
+    static_assert((RG - 1) * 2 * 64 * 16 <= 2 * kBuf, "partials fit one range's buffers");
+    __shared__ __attribute__((aligned(16))) uint8_t lds_all[RG * 2 * kBuf];
+    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, nst = (nblk + SB - 1) / SB;
+    const int L = (nst + RG - 1) / RG;  // stages per range
     const int mt = (M + BM - 1) / BM;
     const int total = (int)gridDim.x;
     int tile = (int)blockIdx.x;
     if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
     const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
 
-    const int tid = (int)threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = (int)threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int p = wv >> 1, wave = wv & 1;  // K range, column half
+    const int tid = (int)threadIdx.x & 127;  // thread within the range's pair of waves
     const int r16 = lane & 15, g = lane >> 4;
+    uint8_t *const lds = lds_all + p * 2 * kBuf;
+    const int kbs = p * L * SB;                                        // first block of the range
+    const int ns = nst - p * L < L ? (nst - p * L > 0 ? nst - p * L : 0) : L;  // stages of the range
 
     // X: thread t stages 16-byte chunk t % 8 of tile row t / 8; W: chunks t + 128 j.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(xq, (uint64_t)M * (uint64_t)K);
@@ -909,7 +921,7 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
     Set set[R];
     auto load = [&](int i, Set &S_) {
         const bool live = i < ns;
-        const int kb0 = i * SB, k0 = kb0 * 32;
+        const int kb0 = kbs + i * SB, k0 = kb0 * 32;
         S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, live && k0 + xc * 16 < K ? xoff : kOob, (uint32_t)k0, 0));
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -968,7 +980,7 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
     // Iteration i: the barrier publishes stage i (stored during iteration i - 1) and frees
     // the other buffer; the loads of stage i + R go into the set stage i came from; stage
     // i + 1 is stored while stage i is computed.
-    for (int i0 = 0; i0 < ns; i0 += R) {
+    for (int i0 = 0; i0 < L; i0 += R) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int i = i0 + r;  // i0 is a multiple of the even R: buffer i % 2 == r % 2
@@ -977,8 +989,10 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
             __builtin_amdgcn_sched_barrier(0);
             store(set[(r + 1) % R], (r + 1) & 1);
             const uint8_t *b = lds + (r & 1) * kBuf;
-            const int kb0 = i * SB;
-            if (kb0 + SB <= nblk) {
+            const int kb0 = kbs + i * SB;
+            if (i >= ns) {
+                // past the range: nothing to fold
+            } else if (kb0 + SB <= nblk) {
                 i32x4s I[SB];
 #pragma unroll
                 for (int kb = 0; kb < SB; kb++) I[kb] = mfma(b, kb);
@@ -990,10 +1004,25 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
         }
     }
     const int col = n0 + rb;
+    if constexpr (RG == 1) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = m0 + 4 * g + j;
+            if (row < M && col < N) y[(int64_t)row * N + col] = acc[j];
+        }
+        return;
+    }
+    // ---- the partials of ranges 1, 2, 3 go through LDS; range 0 adds them in order
+    __syncthreads();
+    f32x4 *red = reinterpret_cast<f32x4 *>(lds_all);
+    if (p > 0) red[((p - 1) * 2 + wave) * 64 + lane] = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    __syncthreads();
+    if (p > 0) return;
+    const f32x4 p1 = red[wave * 64 + lane], p2 = red[(2 + wave) * 64 + lane], p3 = red[(4 + wave) * 64 + lane];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int row = m0 + 4 * g + j;
-        if (row < M && col < N) y[(int64_t)row * N + col] = acc[j];
+        if (row < M && col < N) y[(int64_t)row * N + col] = ((acc[j] + p1[j]) + p2[j]) + p3[j];
     }
 }
 

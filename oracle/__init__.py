@@ -55,6 +55,7 @@ def load():
             "ref_bf16_to_f32": [C.c_uint16],
             "ref_quantize_act": [_vp, _i64, _i64, _vp, _vp],
             "ref_gemm_q8_int8_emulated": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+            "ref_gemm_q8_int8_emulated_ranges": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp],
             "ref_gemm_q8_f64": [_vp, _vp, _i64, _i64, _i64, _vp],
             "ref_gemm_q8_bf16w_f64": [_vp, _vp, _i64, _i64, _i64, _vp],
         }
@@ -134,9 +135,12 @@ def quantize_act(x_bf16: np.ndarray, m: int, k: int):
     return q, s
 
 
-def gemm_int8_emulated(xq, xs, w_blob, m, n, k) -> np.ndarray:
+def gemm_int8_emulated(xq, xs, w_blob, m, n, k, ranges: int = 1, stage_blocks: int = 4) -> np.ndarray:
+    """Emulated int8 GEMM; ranges > 1 cuts K into that many contiguous ranges of whole
+    stages, folds each into its own partial and adds the partials in order."""
     y = np.empty((m, n), dtype=np.float32)
-    _ok(load().ref_gemm_q8_int8_emulated(_p(np.ascontiguousarray(xq)), _p(np.ascontiguousarray(xs)), _p(w_blob), m, n, k, _p(y)), "gemm_int8")
+    _ok(load().ref_gemm_q8_int8_emulated_ranges(_p(np.ascontiguousarray(xq)), _p(np.ascontiguousarray(xs)), _p(w_blob), m, n,
+                                                k, ranges, stage_blocks if ranges > 1 else 1, _p(y)), "gemm_int8")
     return y
 
 

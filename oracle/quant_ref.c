@@ -331,25 +331,34 @@ int ref_quantize_act(const uint16_t *x_bf16, int64_t m, int64_t k, int8_t *q, fl
     return 0;
 }
 
-int ref_gemm_q8_int8_emulated(const int8_t *xq, const float *xs, const uint8_t *w_blob, int64_t m, int64_t n,
-                              int64_t k, float *y) {
-    if (m <= 0 || n <= 0 || k <= 0 || k % 32 != 0) return -1;
+int ref_gemm_q8_int8_emulated_ranges(const int8_t *xq, const float *xs, const uint8_t *w_blob, int64_t m,
+                                     int64_t n, int64_t k, int64_t nranges, int64_t stage_blocks, float *y) {
+    if (m <= 0 || n <= 0 || k <= 0 || k % 32 != 0 || nranges < 1 || nranges > 8 || stage_blocks < 1) return -1;
     const int64_t nb = k / 32;
+    const int64_t stages = (nb + stage_blocks - 1) / stage_blocks;
+    const int64_t span = (stages + nranges - 1) / nranges * stage_blocks; /* blocks per range */
     for (int64_t i = 0; i < m; i++) {
         for (int64_t j = 0; j < n; j++) {
-            float acc = 0.0f;
+            float part[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
             for (int64_t b = 0; b < nb; b++) {
                 const uint8_t *wb = w_blob + (j * nb + b) * 34;
                 const int8_t *xb = xq + i * k + b * 32;
                 int32_t dot = 0;
                 for (int t = 0; t < 32; t++) dot += (int32_t)xb[t] * (int32_t)(int8_t)wb[2 + t];
                 const float s = xs[i * nb + b] * half_at(wb);
-                acc = fmaf((float)dot, s, acc);
+                part[b / span] = fmaf((float)dot, s, part[b / span]);
             }
+            float acc = part[0];
+            for (int64_t p = 1; p < nranges; p++) acc = acc + part[p];
             y[i * n + j] = acc;
         }
     }
     return 0;
+}
+
+int ref_gemm_q8_int8_emulated(const int8_t *xq, const float *xs, const uint8_t *w_blob, int64_t m, int64_t n,
+                              int64_t k, float *y) {
+    return ref_gemm_q8_int8_emulated_ranges(xq, xs, w_blob, m, n, k, 1, 1, y);
 }
 
 static int gemm_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k, double *y,

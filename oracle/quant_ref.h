@@ -69,6 +69,12 @@ int ref_quantize_act(const uint16_t *x_bf16, int64_t m, int64_t k, int8_t *q, fl
  * W is Q8_0 [n, k]. The tight (bit-exact) check for the int8 path. */
 int ref_gemm_q8_int8_emulated(const int8_t *xq, const float *xs, const uint8_t *w_blob,
                               int64_t m, int64_t n, int64_t k, float *y);
+/* The same with K cut into nranges contiguous ranges of whole stages (stage_blocks blocks
+ * each; every range but the last ceil(stages / nranges) stages): each range folds its blocks
+ * in order into its own partial from 0, then y = ((p0 + p1) + p2) + ... (nranges = 1: the
+ * above). The GPU's small-M int8 kernel uses four ranges of four-block stages. */
+int ref_gemm_q8_int8_emulated_ranges(const int8_t *xq, const float *xs, const uint8_t *w_blob, int64_t m,
+                                     int64_t n, int64_t k, int64_t nranges, int64_t stage_blocks, float *y);
 /* Exact reference for both GEMM variants: Y = X_bf16 . dequant(W)^T in double. */
 int ref_gemm_q8_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k, double *y);
 /* bf16 variant emulation: Y = X_bf16 . bf16(dequant(W))^T in double. */

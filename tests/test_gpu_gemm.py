@@ -46,6 +46,13 @@ def bits(a):
     return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
 
 
+def int8_ranges(m, n, k):
+    """K ranges of the int8 kernel the dispatch picks: four on the small-M kernel (M <= 256,
+    N % 8 == 0) when it has at most 256 16 x 32 tiles, else one fold over all of K."""
+    tiles = -(-m // 16) * -(-n // 32)
+    return 4 if m <= 256 and n % 8 == 0 and n * k < 2**31 and tiles <= 256 else 1
+
+
 def rel_err(y, ref):
     return float(np.abs(y.astype(np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
 
@@ -82,7 +89,7 @@ def test_gemm_int8_matches_emulation_bit_exact(backend, m, n, k):
     assert y.shape == (m, n)
     got = backend.download(y).reshape(m, n)
     xq, xs = oracle.quantize_act(xb, m, k)
-    emu = oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k)
+    emu = oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k, ranges=int8_ranges(m, n, k))
     assert np.array_equal(bits(got), bits(emu))
     assert rel_err(got, oracle.gemm_f64(xb, w_blob, m, n, k)) <= TOL_BF16X
     for h in (w, x, y):
@@ -103,10 +110,12 @@ def test_gemm_bf16_matches_reference(backend, m, n, k):
 
 # The int8 kernels with N % 8 == 0 (stages of four blocks): one block; a partial last stage
 # (K = 96, 160, 800); tails in M and N; the benchmark K; both sides of the M = 256 switch
-# between the 16 x 32 and 64 x 128 tile kernels. Every case is bit-identical to the
-# emulation, which folds blocks in order.
+# between the 16 x 32 and 64 x 128 tile kernels, and on the 16 x 32 kernel both sides of
+# its 256-tile switch between four K ranges (K = 800, 2080, 4096: uneven ranges) and one
+# ((96, 3000): 564 tiles). Every case is bit-identical to the emulation with the same
+# association (blocks in order within each range, ranges added in order).
 INT8_WIDE_SHAPES = [(65, 8, 32), (512, 136, 96), (600, 1024, 4096), (2048, 256, 160), (100, 48, 800),
-                    (7, 40, 4096), (256, 64, 1024), (257, 64, 1024), (30, 1000, 2080)]
+                    (7, 40, 4096), (256, 64, 1024), (257, 64, 1024), (30, 1000, 2080), (96, 3000, 160)]
 
 
 @pytest.mark.parametrize("m,n,k", INT8_WIDE_SHAPES)
@@ -116,7 +125,7 @@ def test_gemm_int8_wide_tiles_bit_exact(backend, m, n, k):
     y = backend.quant_matmul(w, x, "int8")
     got = backend.download(y).reshape(m, n)
     xq, xs = oracle.quantize_act(xb, m, k)
-    assert np.array_equal(bits(got), bits(oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k)))
+    assert np.array_equal(bits(got), bits(oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k, ranges=int8_ranges(m, n, k))))
     for h in (w, x, y):
         backend.release(h)
 

@@ -243,6 +243,23 @@ def test_gemm_references_against_exact_integer_arithmetic():
             want[i, j] = acc
     got = oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k)
     assert np.array_equal(bits(got), bits(want))
+    # four contiguous ranges of whole 4-block stages (8 blocks = 2 stages: one stage each for
+    # ranges 0 and 1, none for 2 and 3), each folded from 0, partials added in order
+    want4 = np.zeros((m, n), np.float32)
+    for i in range(m):
+        for j in range(n):
+            part = [np.float32(0.0)] * 4
+            for b in range(nb):
+                p = b // 4
+                part[p] = _f32_rne(Fraction(int(dots[i, j, b])) * Fraction(float(scale[i, j, b])) + Fraction(float(part[p])))
+            acc = part[0]
+            for p in range(1, 4):
+                acc = _f32_rne(Fraction(float(acc)) + Fraction(float(part[p])))
+            want4[i, j] = acc
+    got4 = oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k, ranges=4)
+    assert np.array_equal(bits(got4), bits(want4))
+    # the association matters at this size (else the check above would not tell them apart)
+    assert not np.array_equal(bits(got4), bits(got))
 
     xf = (xb.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
     wdq = np_dequant(QuantType.Q8_0, w_blob, n, k).astype(np.float64)
