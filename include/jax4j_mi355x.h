@@ -132,12 +132,18 @@ int j4q_download_bytes(j4q_buffer buffer, void *out, uint64_t nbytes);
 int j4q_buffer_info(j4q_buffer buffer, j4q_buffer_desc *out);
 /* ComputeBackend.release (spi/ComputeBackend.java:280). Releasing 0 is a no-op. */
 int j4q_release(j4q_buffer buffer);
+/* Live buffer handles and the device bytes they hold (engine-local accounting, the
+ * counterpart of the reference's Cleaner-tracked HipBuffer frees, rocm/HipBuffer.java:31-81):
+ * a call that fails after allocating releases what it allocated, so this stays unchanged. */
+int j4q_buffer_stats(int64_t *live, uint64_t *device_bytes);
 
 /* ---- the quantized ops (spi/QuantizedOps.java:27-33) ----------------------------------- */
 
 /* QuantizedOps.quantMatvec (QuantizedOps.java:27; CpuBackend.java:708-725).
  * x with exactly cols elements (any rank) -> y F32 [rows]. Engine extension: x of shape
- * [B, cols] with B > 1 -> y F32 [B, rows] (row b of y is quantMatvec of row b of x). */
+ * [B, cols] with B > 1 -> y F32 [B, rows] (row b of y is quantMatvec of row b of x).
+ * Any block-aligned cols (CpuQ4Gemm.java:79-83): up to 32768 columns one launch holds x in
+ * LDS; wider matrices run as column windows, each adding the previous window's sums. */
 int j4q_quant_matvec(j4q_buffer weights, j4q_buffer x, j4q_buffer *y);
 /* QuantizedOps.quantMatvecAdd (QuantizedOps.java:30; CpuBackend.java:728-736):
  * y = (W.x) + add, the add rounded separately. add needs at least as many elements as y. */
@@ -161,7 +167,9 @@ int j4q_quant_matmul(j4q_buffer weights, j4q_buffer x, int variant, j4q_buffer *
 /* ---- stream-ordered entry points on caller memory (no allocation, no sync) ------------- */
 
 /* quantMatvec / quantMatvecAdd into caller device memory: x_dev [batch, cols] and y_dev
- * [batch, rows] fp32 (16-byte aligned); add_dev NULL or [batch, rows]. */
+ * [batch, rows] fp32 (16-byte aligned); add_dev NULL or [batch, rows]. add_dev may be y_dev
+ * itself (a residual updated in place) for cols <= 32768; above that an add overlapping y
+ * returns J4Q_EUNSUPPORTED (the column windows would read it after rewriting y). */
 int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *add_dev, float *y_dev,
                           int64_t batch, void *stream);
 /* Prefill GEMM into caller memory. x_dev bf16 [m, cols]; y_dev fp32 [m, rows]. The int8

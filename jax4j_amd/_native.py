@@ -102,6 +102,7 @@ SIGNATURES = {
     "j4q_download_bytes": [_buf, _vp, _u64],
     "j4q_buffer_info": [_buf, C.POINTER(BufferDesc)],
     "j4q_release": [_buf],
+    "j4q_buffer_stats": [C.POINTER(_i64), C.POINTER(_u64)],
     "j4q_quant_matvec": [_buf, _buf, _pbuf],
     "j4q_quant_matvec_add": [_buf, _buf, _buf, _pbuf],
     "j4q_quant_gather_row": [_buf, _i64, _pbuf],

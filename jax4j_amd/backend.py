@@ -240,6 +240,12 @@ class Mi355xBackend:
         check(N.load().j4q_buffer_info(buffer.handle, C.byref(d)), "buffer_info")
         return d
 
+    def buffer_stats(self) -> tuple:
+        """(live buffer handles, device bytes they hold)."""
+        n, b = C.c_int64(), C.c_uint64()
+        check(self._lib().j4q_buffer_stats(C.byref(n), C.byref(b)), "buffer_stats")
+        return n.value, b.value
+
     def stream(self) -> int:
         s = C.c_void_p()
         check(self._lib().j4q_stream(C.byref(s)), "stream")

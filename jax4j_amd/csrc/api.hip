@@ -14,7 +14,7 @@
 #include "synth.h"
 
 namespace j4q {
-int64_t gemv_max_cols();
+int64_t gemv_single_pass_cols();
 void gemv_set_cus(int cus);
 }
 
@@ -164,6 +164,29 @@ int alloc_buf(int kind, int rank, int64_t d0, int64_t d1, uint64_t bytes, j4q_bu
     return J4Q_OK;
 }
 
+// Undoes alloc_buf after a failed launch: frees the memory, retires the handle and clears
+// *out, so a rejected call leaves no live buffer behind.
+void drop_buf(j4q_buffer *out) {
+    Buf *b = lookup(*out);
+    if (b) {
+        if (b->dev) (void)hipFree(b->dev);
+        b->dev = nullptr;
+        b->live = false;
+        g_free.push_back((uint32_t)((*out & 0xffffffffu) - 1));
+    }
+    *out = 0;
+}
+
+// Launches into a buffer alloc_buf just registered; on failure the buffer is dropped again.
+#define LAUNCH_INTO(op, out, expr)                 \
+    do {                                           \
+        hipError_t e_ = (expr);                    \
+        if (e_ != hipSuccess) {                    \
+            drop_buf(out);                         \
+            return hip_fail(op, e_);               \
+        }                                          \
+    } while (0)
+
 int check_quant_args(int qt, uint64_t nbytes, int64_t rows, int64_t cols, Geometry *g) {
     if (!j4q::geometry_of(qt, g)) {
         const int known[] = {0, 1, 2, 8, 12, 14, 30, 41, 42};
@@ -254,10 +277,7 @@ int upload_dense(int kind, int elem_bytes, const void *data, int32_t rank, const
         hipError_t e = hipMemcpyAsync(dev, data, bytes, hipMemcpyHostToDevice, g_stream);
         if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
         if (e != hipSuccess) {
-            (void)hipFree(dev);
-            lookup(*out)->live = false;
-            g_free.push_back((uint32_t)((*out & 0xffffffffu) - 1));
-            *out = 0;
+            drop_buf(out);
             return hip_fail("upload", e);
         }
     }
@@ -293,9 +313,6 @@ int matvec_common(j4q_buffer wh, j4q_buffer xh, j4q_buffer addh, j4q_buffer *out
     const int64_t N = w->dims[0];
     if (add && elements_of(*add) < B * N)
         return fail(J4Q_EINVAL, "%s: add has %lld elements, needs %lld", op, (long long)elements_of(*add), (long long)(B * N));
-    if (w->dims[1] > j4q::gemv_max_cols())
-        return fail(J4Q_EUNSUPPORTED, "%s: cols=%lld exceeds the GEMV limit %lld", op, (long long)w->dims[1],
-                    (long long)j4q::gemv_max_cols());
     if (B > 65535) return fail(J4Q_EUNSUPPORTED, "%s: batch %lld exceeds 65535", op, (long long)B);
     if ((rc = ensure_ready())) return rc;
     const void *xdev = x->dev, *adev = add ? add->dev : nullptr;
@@ -304,7 +321,17 @@ int matvec_common(j4q_buffer wh, j4q_buffer xh, j4q_buffer addh, j4q_buffer *out
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, B == 1 ? 1 : 2, B == 1 ? N : B, B == 1 ? 0 : N, (uint64_t)(B * N) * 4, out, &ydev)))
         return rc;
-    HIP_TRY(op, j4q::launch_gemv(qt, m, (const float *)xdev, (const float *)adev, (float *)ydev, B, g_stream));
+    LAUNCH_INTO(op, out, j4q::launch_gemv(qt, m, (const float *)xdev, (const float *)adev, (float *)ydev, B, g_stream));
+    return J4Q_OK;
+}
+
+// Size limits of the prefill GEMM kernels (32-bit element offsets into X and W, grid
+// dimensions), checked before anything is allocated.
+int check_gemm_size(int64_t M, int64_t K, int variant, const char *op) {
+    const uint64_t xbytes = (uint64_t)M * (uint64_t)K * (variant == J4Q_GEMM_BF16 ? 2u : 1u);
+    if (M > 65535 * 64 || xbytes > 0x7fffffffull)
+        return fail(J4Q_EUNSUPPORTED, "%s: M = %lld, K = %lld exceeds the GEMM limits (M <= %d, X under 2 GiB)", op,
+                    (long long)M, (long long)K, 65535 * 64);
     return J4Q_OK;
 }
 
@@ -539,6 +566,21 @@ int j4q_buffer_info(j4q_buffer h, j4q_buffer_desc *out) {
     return J4Q_OK;
 }
 
+int j4q_buffer_stats(int64_t *live, uint64_t *bytes) {
+    if (!live || !bytes) return fail(J4Q_EINVAL, "buffer_stats: NULL argument");
+    std::lock_guard<std::mutex> lk(g_mu);
+    int64_t n = 0;
+    uint64_t b = 0;
+    for (const Buf &x : g_bufs)
+        if (x.live) {
+            n++;
+            b += x.bytes;
+        }
+    *live = n;
+    *bytes = b;
+    return J4Q_OK;
+}
+
 int j4q_release(j4q_buffer h) {
     if (h == 0) return J4Q_OK;
     std::lock_guard<std::mutex> lk(g_mu);
@@ -577,7 +619,7 @@ int j4q_quant_gather_row(j4q_buffer wh, int64_t row, j4q_buffer *out) {
     const int64_t K = w->dims[1];
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, 1, K, 0, (uint64_t)K * 4, out, &ydev))) return rc;
-    HIP_TRY("quantGatherRow", j4q::launch_dequant_rows(qt, m, row, 1, (float *)ydev, g_stream));
+    LAUNCH_INTO("quantGatherRow", out, j4q::launch_dequant_rows(qt, m, row, 1, (float *)ydev, g_stream));
     return J4Q_OK;
 }
 
@@ -593,7 +635,7 @@ int j4q_quant_dequantize(j4q_buffer wh, j4q_buffer *out) {
     const int64_t N = w->dims[0], K = w->dims[1];
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, 2, N, K, (uint64_t)(N * K) * 4, out, &ydev))) return rc;
-    HIP_TRY("dequantize", j4q::launch_dequant_rows(qt, m, 0, N, (float *)ydev, g_stream));
+    LAUNCH_INTO("dequantize", out, j4q::launch_dequant_rows(qt, m, 0, N, (float *)ydev, g_stream));
     return J4Q_OK;
 }
 
@@ -610,8 +652,16 @@ int j4q_quantize_act(j4q_buffer xh, j4q_buffer *xq, j4q_buffer *xs) {
     const void *xdev = x->dev;
     void *qdev, *sdev;
     if ((rc = alloc_buf(J4Q_KIND_I8, 2, M, K, (uint64_t)(M * K), xq, &qdev))) return rc;
-    if ((rc = alloc_buf(J4Q_KIND_F32, 2, M, K / 32, (uint64_t)(M * (K / 32)) * 4, xs, &sdev))) return rc;
-    HIP_TRY("quantize_act", j4q::launch_quantize_act((const uint16_t *)xdev, M, K, (int8_t *)qdev, (float *)sdev, g_stream));
+    if ((rc = alloc_buf(J4Q_KIND_F32, 2, M, K / 32, (uint64_t)(M * (K / 32)) * 4, xs, &sdev))) {
+        drop_buf(xq);
+        return rc;
+    }
+    const hipError_t e = j4q::launch_quantize_act((const uint16_t *)xdev, M, K, (int8_t *)qdev, (float *)sdev, g_stream);
+    if (e != hipSuccess) {
+        drop_buf(xq);
+        drop_buf(xs);
+        return hip_fail("quantize_act", e);
+    }
     return J4Q_OK;
 }
 
@@ -627,6 +677,7 @@ int j4q_quant_matmul(j4q_buffer wh, j4q_buffer xh, int variant, j4q_buffer *out)
     if (x->rank != 2 || x->dims[1] != w->dims[1] || x->dims[0] <= 0)
         return fail(J4Q_EINVAL, "quantMatmul shape mismatch: [%lld, %lld] x [%lld, %lld]", (long long)w->dims[0],
                     (long long)w->dims[1], (long long)x->dims[0], (long long)(x->rank == 2 ? x->dims[1] : 0));
+    if ((rc = check_gemm_size(x->dims[0], w->dims[1], variant, "quantMatmul"))) return rc;
     if ((rc = ensure_ready())) return rc;
     const int64_t M = x->dims[0], N = w->dims[0], K = w->dims[1];
     const j4q::QMat m = qmat_of(*w);
@@ -634,18 +685,18 @@ int j4q_quant_matmul(j4q_buffer wh, j4q_buffer xh, int variant, j4q_buffer *out)
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, 2, M, N, (uint64_t)(M * N) * 4, out, &ydev))) return rc;
     if (variant == J4Q_GEMM_BF16) {
-        HIP_TRY("quantMatmul", j4q::launch_gemm_q8_bf16(m, xdev, (float *)ydev, M, g_stream));
+        LAUNCH_INTO("quantMatmul", out, j4q::launch_gemm_q8_bf16(m, xdev, (float *)ydev, M, g_stream));
         return J4Q_OK;
     }
     void *ws = nullptr;
     const uint64_t qbytes = (uint64_t)(M * K), sbytes = (uint64_t)(M * (K / 32)) * 4;
-    HIP_TRY("hipMalloc", hipMallocAsync(&ws, qbytes + sbytes + 256, g_stream));
+    LAUNCH_INTO("hipMallocAsync", out, hipMallocAsync(&ws, j4q::align256(qbytes) + sbytes, g_stream));
     int8_t *xq = (int8_t *)ws;
     float *xs = (float *)((uint8_t *)ws + j4q::align256(qbytes));
     hipError_t e = j4q::launch_quantize_act(xdev, M, K, xq, xs, g_stream);
     if (e == hipSuccess) e = j4q::launch_gemm_q8_int8(m, xq, xs, (float *)ydev, M, g_stream);
     (void)hipFreeAsync(ws, g_stream);
-    if (e != hipSuccess) return hip_fail("quantMatmul", e);
+    LAUNCH_INTO("quantMatmul", out, e);
     return J4Q_OK;
 }
 
@@ -658,8 +709,11 @@ int j4q_quant_matvec_into(j4q_buffer wh, const float *x, const float *add, float
     Buf *w;
     int rc;
     if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatvec_into", &w))) return rc;
-    if (w->dims[1] > j4q::gemv_max_cols())
-        return fail(J4Q_EUNSUPPORTED, "quantMatvec_into: cols=%lld exceeds the GEMV limit %lld", (long long)w->dims[1], (long long)j4q::gemv_max_cols());
+    const int64_t N = w->dims[0], K = w->dims[1];
+    if (add && add < y + batch * N && y < add + batch * N && K > j4q::gemv_single_pass_cols())
+        return fail(J4Q_EUNSUPPORTED,
+                    "quantMatvec_into: an add that overlaps y needs cols <= %lld (one column window), got %lld",
+                    (long long)j4q::gemv_single_pass_cols(), (long long)K);
     if ((rc = ensure_ready())) return rc;
     HIP_TRY("quantMatvec_into", j4q::launch_gemv(w->qtype, qmat_of(*w), x, add, y, batch, pick_stream(stream)));
     return J4Q_OK;
@@ -678,6 +732,7 @@ int j4q_quant_matmul_into(j4q_buffer wh, const uint16_t *x, int64_t m, int varia
     int rc;
     if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatmul_into", &w))) return rc;
     if (w->qtype != J4Q_Q8_0) return fail(J4Q_EUNSUPPORTED, "quantMatmul_into: only Q8_0 weights are supported");
+    if ((rc = check_gemm_size(m, w->dims[1], variant, "quantMatmul_into"))) return rc;
     if ((rc = ensure_ready())) return rc;
     const hipStream_t s = pick_stream(stream);
     const j4q::QMat mm = qmat_of(*w);

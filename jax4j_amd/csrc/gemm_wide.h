@@ -1,5 +1,5 @@
-// Prefill GEMM, bf16 variant for M >= 512: Y[M, N] = X[M, K] . bf16(W)[N, K]^T over Q8_0
-// weights, fp32 output.
+// Prefill GEMM, bf16 variant, register-staged (odd N at M >= 512): Y[M, N] = X[M, K] .
+// bf16(W)[N, K]^T over Q8_0 weights, fp32 output.
 //
 // Tile BM x 64 NJ (BM = 64 or 128, NJ = 1 or 2) per workgroup of 8 waves, two waves per
 // SIMD. K advances in stages of 64 (two Q8_0 blocks); wave w owns columns
@@ -297,7 +297,8 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Prefill GEMM, bf16 variant for M >= 512 and even N, results bit-identical to
+// Prefill GEMM, bf16 variant for even N from M = 65 on (whenever its grid has at least 128
+// workgroups; launch_gemm_q8_bf16 in gemm.hip picks the tile), results bit-identical to
 // gemm_bf16_wide (the same blocks go to the same waves in the same order):
 //  - Tile BM x 64 NJ per workgroup of 8 waves; wave w owns columns [16 NJ (w % 4), +16 NJ)
 //    and blocks 2 b + w / 4 (b = 0, 1) of every 128-k stage, for all BM rows.

@@ -5,23 +5,42 @@
 
 namespace j4q {
 
-// Largest K whose x image (K floats + K/16 sums) fits the 64 KiB of LDS a workgroup may use.
-int64_t gemv_max_cols() { return 15360; }
+// Widest K one vector-ALU launch covers (x image in LDS); a wider K runs as column windows.
+int64_t gemv_single_pass_cols() { return gemv::kMaxWindow; }
 
 namespace {
 
 // Launch shape, from measured sweeps on MI355X (one row per group, two register sets in
-// flight, ~62 VGPRs per wave): for K <= 4096, 8 waves per workgroup and 4 workgroups per CU
-// (8 waves per SIMD: ~5 % faster than 4, the extra waves fill the gaps the unpack leaves in
-// the memory stream); for K <= 8192, 2 workgroups per CU; for larger K (an x image of up to
-// 64 KiB), 16 waves in one workgroup per CU. The grid never exceeds what is resident at
-// once, so x is staged once per workgroup.
+// flight, ~62 VGPRs per wave): for windows of K <= 4096, 8 waves per workgroup and 4
+// workgroups per CU (8 waves per SIMD: ~5 % faster than 4, the extra waves fill the gaps
+// the unpack leaves in the memory stream); for K <= 8192, 2 workgroups per CU; for larger
+// windows (an x image of up to 139 KB), 16 waves in one workgroup per CU. The grid never
+// exceeds what is resident at once, so x is staged once per workgroup.
 template <int FMT>
-hipError_t launch_fmt(const QMat &m, const float *x, const float *add, float *y, int batch, int cus,
-                      hipStream_t s) {
-    if (m.cols <= 4096) return gemv::launch<FMT, 1, 8, 2>(m, x, add, y, batch, 4 * cus, s);
-    if (m.cols <= 8192) return gemv::launch<FMT, 1, 8, 2>(m, x, add, y, batch, 2 * cus, s);
-    return gemv::launch<FMT, 1, 16, 2>(m, x, add, y, batch, cus, s);
+hipError_t launch_window(const QMat &m, const float *x, const float *prev, const float *add, float *y, int batch,
+                         int cus, int64_t c0, int64_t kw, hipStream_t s) {
+    if (kw <= 4096) return gemv::launch<FMT, 1, 8, 2>(m, x, prev, add, y, batch, 4 * cus, c0, kw, s);
+    if (kw <= 8192) return gemv::launch<FMT, 1, 8, 2>(m, x, prev, add, y, batch, 2 * cus, c0, kw, s);
+    return gemv::launch<FMT, 1, 16, 2>(m, x, prev, add, y, batch, cus, c0, kw, s);
+}
+
+// K up to 32768 in one launch; wider K as equal windows of whole 2048-column steps, each
+// adding the previous window's y (prev), the caller's add joining only in the last one.
+// Callers keep an add that overlaps y to a single window (it would be read after y was
+// rewritten).
+template <int FMT>
+hipError_t launch_fmt(const QMat &m, const float *x, const float *add, float *y, int batch, int cus, hipStream_t s) {
+    const int64_t K = m.cols;
+    if (K <= gemv::kMaxWindow) return launch_window<FMT>(m, x, nullptr, add, y, batch, cus, 0, K, s);
+    const int64_t windows = (K + gemv::kMaxWindow - 1) / gemv::kMaxWindow;
+    const int64_t per = ((K + windows - 1) / windows + 2047) / 2048 * 2048;
+    for (int64_t c0 = 0; c0 < K; c0 += per) {
+        const int64_t kw = K - c0 < per ? K - c0 : per;
+        const bool last = c0 + kw >= K;
+        const hipError_t e = launch_window<FMT>(m, x, c0 ? y : nullptr, last ? add : nullptr, y, batch, cus, c0, kw, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 int g_cus = 256;
@@ -121,8 +140,9 @@ void gemv_set_cus(int cus) { g_cus = cus > 0 ? cus : 256; }
 hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, float *y, int64_t batch,
                        hipStream_t s) {
     if (m.rows <= 0 || batch <= 0) return hipSuccess;
-    if (m.cols > gemv_max_cols() || batch > 65535 || m.rows > (1 << 30)) return hipErrorInvalidValue;
+    if (batch > 65535 || m.rows > (1 << 30) || m.cols > 0x7fffffff) return hipErrorInvalidValue;
     const bool alias = add && add < y + batch * m.rows && y < add + batch * m.rows;
+    if (alias && m.cols > gemv::kMaxWindow) return hipErrorInvalidValue;
     if (batch < 3 || !mfma_supported(id, m, alias)) return launch_valu(id, m, x, add, y, (int)batch, s);
     // batch rows in launches of up to 16 on the matrix cores (9..16 rows stream W once, in
     // windows of 2048 columns); a remainder of 1 or 2 rows takes the vector-ALU kernel,

@@ -321,8 +321,12 @@ struct Chunk<Q6_K> {
         q6_dot(q, h, x, slo, shi);
         const float df = half_bits_to_float(d);
         const float da = df * (float)(int8_t)(s & 0xFF), db = df * (float)(int8_t)(s >> 8);
-        acc = __builtin_fmaf(da, __builtin_fmaf(slo, kTwo24, -32.0f * sx.x), acc);
-        return __builtin_fmaf(db, __builtin_fmaf(shi, 1048576.0f, -32.0f * sx.y), acc);
+        // sum (q - 32) x stays in the fields' units (2^-24 low, 2^-20 high) and the restoring
+        // power of two rides on the scale: sum (q - 32) x itself exceeds fp32 for |x| above
+        // ~6e35 where d * sc * sum (q - 32) x does not. Powers of two scale exactly, so the
+        // result is the same as restoring first.
+        acc = __builtin_fmaf(da * kTwo24, __builtin_fmaf(sx.x, -0x1p-19f, slo), acc);
+        return __builtin_fmaf(db * 1048576.0f, __builtin_fmaf(sx.y, -0x1p-15f, shi), acc);
     }
 };
 
@@ -355,19 +359,24 @@ __device__ __forceinline__ Rsrc rsrc_of(const QMat &m, int fmt) {
 }
 
 // grid: (G workgroups of WAVES waves, batch); groups = ceil(N / R). Dynamic LDS:
-// XImage<NP>::kBytes. Requires K % 32 == 0, K / 32 <= NP, K / 4 <= XU * WAVES * 64 and every
-// section < 2^31 bytes.
+// XImage<NP>::kBytes. The launch covers the column window [2048 st0, 2048 st0 + KW) of every
+// row: y = (W[:, window] x[window] + prev) + add, so a K wider than one x image runs as
+// windows chained through prev (the previous window's y, read by the wave that rewrites that
+// element) with the caller's add joining only in the last window. Requires KW % 32 == 0,
+// KW / 32 <= NP, KW / 4 <= XU * WAVES * 64 and every section < 2^31 bytes.
 template <int FMT, int R, int WAVES, int D, int XU, int NP>
 __global__ void __launch_bounds__(WAVES * 64)
-gemv_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, float *__restrict__ y, int groups) {
+gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float *add, float *y, int groups, int st0,
+            int KW) {
     extern __shared__ f32x4 lds[];
     const int K = (int)m.cols, N = (int)m.rows;
     // blockIdx.y selects a batch row (each batch row streams W again; batched decode uses
     // the MFMA kernel instead).
-    x += (int64_t)blockIdx.y * K;
+    x += (int64_t)blockIdx.y * K + (int64_t)st0 * 2048;
     y += (int64_t)blockIdx.y * N;
     if (add) add += (int64_t)blockIdx.y * N;
-    const int nchunks = K / 32, cpl = (nchunks + 63) / 64;
+    if (prev) prev += (int64_t)blockIdx.y * N;
+    const int nchunks = KW / 32, cpl = (nchunks + 63) / 64;
     // The wave index is uniform; saying so keeps every row/step offset in SGPRs (a buffer
     // load with a VGPR soffset would need a waterfall loop).
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -385,7 +394,7 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, 
     // separates a load from its use, and each wait leaves the other sets' loads in flight.
     auto load_item = [&](int i, Chunk<FMT> (&ch)[R]) {
         const int q = i / cpl;
-        const int st = i - q * cpl;
+        const int st = i - q * cpl + st0;
         const int g = gw + q * nw;
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -401,7 +410,7 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, 
     };
 
     XStage<WAVES * 64, XU, NP> xst;
-    xst.load(x, K);
+    xst.load(x, KW);
     // D register sets form a ring: set d holds items d, d + D, d + 2D, ...
     Chunk<FMT> set[D][R];
 #pragma unroll
@@ -409,7 +418,7 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, 
 
     f32x4 *xs = lds;
     float *s16 = reinterpret_cast<float *>(lds + 8 * NP);
-    xst.store(K, xs, s16);
+    xst.store(KW, xs, s16);
     __syncthreads();
 
     const float2 *s16v = reinterpret_cast<const float2 *>(s16);
@@ -434,7 +443,10 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, 
                 float v = wave_sum(acc[r]);
                 const int row = __builtin_amdgcn_readfirstlane(g * R + r);
                 if (row < N) {
-                    if (add) v += add[row];  // wave-uniform address: a scalar load
+                    // wave-uniform addresses: scalar loads. prev may be y itself: this wave
+                    // reads the element before its own lane 0 rewrites it.
+                    if (prev) v += prev[row];
+                    if (add) v += add[row];
                     if (lane == 0) y[row] = v;
                 }
                 acc[r] = 0.f;
@@ -456,29 +468,33 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *__restrict__ add, 
 }
 
 template <int FMT, int R, int WAVES, int D, int XU, int NP>
-hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, int batch, int grid, int groups,
-                    hipStream_t s) {
-    gemv_kernel<FMT, R, WAVES, D, XU, NP><<<dim3(grid, batch), WAVES * 64, XImage<NP>::kBytes, s>>>(m, x, add, y, groups);
+hipError_t launch_k(const QMat &m, const float *x, const float *prev, const float *add, float *y, int batch, int grid,
+                    int groups, int st0, int kw, hipStream_t s) {
+    gemv_kernel<FMT, R, WAVES, D, XU, NP><<<dim3(grid, batch), WAVES * 64, XImage<NP>::kBytes, s>>>(m, x, prev, add, y,
+                                                                                                  groups, st0, kw);
     return hipGetLastError();
 }
 
-// The kernel is instantiated for three x-image sizes: K <= 4096, K <= 8192, K <= 15360.
+// Widest column window one launch covers: an x image of 32768 columns takes 139,264 bytes of
+// the 160 KiB of LDS a workgroup may use.
+constexpr int64_t kMaxWindow = 32768;
+
+// One launch over the column window [c0, c0 + kw) (c0 a multiple of 2048). The kernel is
+// instantiated for four x-image sizes: kw <= 4096, 8192, 15360 and 32768.
 template <int FMT, int R, int WAVES, int D>
-hipError_t launch(const QMat &m, const float *x, const float *add, float *y, int batch, int wg_cap,
-                  hipStream_t s) {
+hipError_t launch(const QMat &m, const float *x, const float *prev, const float *add, float *y, int batch, int wg_cap,
+                  int64_t c0, int64_t kw, hipStream_t s) {
     const int groups = (int)((m.rows + R - 1) / R);
     int grid = (groups + WAVES - 1) / WAVES;
     if (grid > wg_cap) grid = wg_cap;
     constexpr int T = WAVES * 64;
-    if (m.cols <= 4096) return launch_k<FMT, R, WAVES, D, (1024 + T - 1) / T, 128>(m, x, add, y, batch, grid, groups, s);
-    if (m.cols <= 8192) return launch_k<FMT, R, WAVES, D, (2048 + T - 1) / T, 256>(m, x, add, y, batch, grid, groups, s);
-    if (m.cols <= 15360) return launch_k<FMT, R, WAVES, D, (3840 + T - 1) / T, 480>(m, x, add, y, batch, grid, groups, s);
+    const int st0 = (int)(c0 / 2048), k = (int)kw;
+    if (c0 % 2048 != 0 || kw % 32 != 0 || kw <= 0) return hipErrorInvalidValue;
+    if (kw <= 4096) return launch_k<FMT, R, WAVES, D, (1024 + T - 1) / T, 128>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
+    if (kw <= 8192) return launch_k<FMT, R, WAVES, D, (2048 + T - 1) / T, 256>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
+    if (kw <= 15360) return launch_k<FMT, R, WAVES, D, (3840 + T - 1) / T, 480>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
+    if (kw <= kMaxWindow) return launch_k<FMT, R, WAVES, D, (8192 + T - 1) / T, 1024>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
     return hipErrorInvalidValue;
-}
-
-// LDS bytes of the x image the kernel uses for K columns.
-inline int64_t x_image_bytes(int64_t K) {
-    return K <= 4096 ? XImage<128>::kBytes : K <= 8192 ? XImage<256>::kBytes : XImage<480>::kBytes;
 }
 
 }  // namespace gemv

@@ -414,10 +414,12 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
 #pragma unroll
     for (int k = 0; k < TS; k++) load_tile(tset[k], avs[k], t0 + k * tstep);
     __builtin_amdgcn_sched_barrier(0);
-    // per-batch-row factor that undoes this wave's x scale and the 2^-24 of the weights
+    // per-batch-row factor that undoes this wave's x scale (2^-e); the 2^24 of the weights is
+    // applied as a separate exact product, since 2^(24 - e) overflows for a slice maximum
+    // of 2^118 or more (e <= -104)
     float wscale[BB];
 #pragma unroll
-    for (int bb = 0; bb < BB; bb++) wscale[bb] = ldexpf(1.0f, 24 - ex[bb]);
+    for (int bb = 0; bb < BB; bb++) wscale[bb] = ldexpf(1.0f, -ex[bb]);
 
     auto A = [&](int bl) -> h8 {
         if constexpr (XREG) return areg[bl];
@@ -586,7 +588,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             float ws = 0.f;
 #pragma unroll
             for (int bb = 0; bb < BB; bb++) ws = (bb == hb + j) ? wscale[bb] : ws;
-            if (hi_lane) pp[(wave * BB + hb + j) * 16 + n] = v * ws;
+            if (hi_lane) pp[(wave * BB + hb + j) * 16 + n] = (v * 16777216.0f) * ws;
         }
         // the tile's prev / add values, fetched with its weights by threads (b, nn)
         if ((int)threadIdx.x < BB * 16) pa[slot * BB * 16 + threadIdx.x] = av;

@@ -50,6 +50,7 @@ def load():
             "ref_dequant_row": [C.c_int, _vp, _i64, _vp],
             "ref_matvec": [C.c_int, _vp, _i64, _i64, _vp, _vp],
             "ref_matvec_f64": [C.c_int, _vp, _i64, _i64, _vp, _vp],
+            "ref_matmul_f64": [C.c_int, _vp, _i64, _i64, _vp, _i64, _vp],
             "ref_dequant_matrix": [C.c_int, _vp, _i64, _i64, _vp],
             "ref_f32_to_bf16": [C.c_float],
             "ref_bf16_to_f32": [C.c_uint16],
@@ -100,6 +101,14 @@ def matvec_f64(qtype: int, blob: np.ndarray, rows: int, cols: int, x: np.ndarray
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty(rows, dtype=np.float64)
     _ok(load().ref_matvec_f64(qtype, _p(blob), rows, cols, _p(x), _p(y)), "matvec_f64")
+    return y
+
+
+def matmul_f64(qtype: int, blob: np.ndarray, rows: int, cols: int, xs: np.ndarray) -> np.ndarray:
+    """matvec_f64 of every row of xs [B, cols] -> [B, rows]; row b equals matvec_f64(xs[b])."""
+    xs = np.ascontiguousarray(xs, dtype=np.float32).reshape(-1, cols)
+    y = np.empty((xs.shape[0], rows), dtype=np.float64)
+    _ok(load().ref_matmul_f64(qtype, _p(blob), rows, cols, _p(xs), xs.shape[0], _p(y)), "matmul_f64")
     return y
 
 

@@ -289,6 +289,29 @@ int ref_matvec_f64(int type_id, const uint8_t *blob, int64_t rows, int64_t cols,
     return 0;
 }
 
+/* ref_matvec_f64 for a batch of B activation rows x[B][cols] -> y[B][rows]: each weight row
+ * is decoded once and dotted with every batch row in the same order as ref_matvec_f64, so
+ * row b equals ref_matvec_f64 of x[b] exactly (semantics: CpuBackend.java:708-725 per row). */
+int ref_matmul_f64(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, const float *x, int64_t batch,
+                   double *y) {
+    int be, bb;
+    if (ref_block_geometry(type_id, &be, &bb) != 0 || !valid_dims(rows, cols, be) || batch <= 0) return -1;
+    float *w = (float *)malloc((size_t)cols * sizeof(float));
+    if (!w) return -1;
+    const int64_t rb = row_bytes_of(type_id, cols);
+    for (int64_t r = 0; r < rows; r++) {
+        ref_dequant_row(type_id, blob + r * rb, cols, w);
+        for (int64_t b = 0; b < batch; b++) {
+            const float *xb = x + b * cols;
+            double sum = 0.0;
+            for (int64_t k = 0; k < cols; k++) sum += (double)w[k] * (double)xb[k];
+            y[b * rows + r] = sum;
+        }
+    }
+    free(w);
+    return 0;
+}
+
 int ref_dequant_matrix(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, float *out) {
     int be, bb;
     if (ref_block_geometry(type_id, &be, &bb) != 0 || !valid_dims(rows, cols, be)) return -1;

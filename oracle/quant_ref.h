@@ -53,6 +53,10 @@ int ref_matvec(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, con
 /* Same product accumulated in double: the brute-force tolerance reference. */
 int ref_matvec_f64(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, const float *x, double *y);
 /* Full-matrix dequantization, rows x cols fp32. */
+/* ref_matvec_f64 over a batch: x [batch][cols] -> y [batch][rows]; row b equals
+ * ref_matvec_f64 of x[b] bit for bit (one decode of each weight row). */
+int ref_matmul_f64(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, const float *x, int64_t batch,
+                   double *y);
 int ref_dequant_matrix(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, float *out);
 
 /* bf16 helpers: round-to-nearest-even fp32 -> bf16, and bf16 -> fp32. */

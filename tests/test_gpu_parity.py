@@ -217,12 +217,12 @@ def test_gemv_batched_matches_oracle(backend, uploaded, qt, rows, cols, B):
     # quantMatvecAdd rounds the add on its own
     assert np.array_equal(bits(gota), bits(got + add))
     # each batch row depends on its own x only: a permuted batch gives the permuted rows.
-    # Rows are launched in groups of 8 (a remainder of 1-2 rows takes the vector-ALU
+    # Rows are launched in groups of up to 16 (a remainder of 1-2 rows takes the vector-ALU
     # kernel, which sums in another order), so the permutation stays inside each group.
     perm = np.arange(B)
-    for c in range(0, B, 8):
-        if min(B, c + 8) - c >= 3:
-            perm[c:c + 8] = np.roll(perm[c:c + 8], 1)
+    for c in range(0, B, 16):
+        if min(B, c + 16) - c >= 3:
+            perm[c:c + 16] = np.roll(perm[c:c + 16], 1)
     xp = backend.upload(np.ascontiguousarray(xs[perm]), shape=(B, cols))
     yp = backend.quant_matvec(w, xp)
     assert np.array_equal(bits(backend.download(yp).reshape(B, rows)), bits(got[perm]))
@@ -318,15 +318,24 @@ def test_gemv_batched_one_hot_and_range(backend, uploaded, qt):
     backend.release(y)
     backend.release(xb)
     # x far outside fp16 range, and far below it: the per-row power-of-two scale keeps the
-    # hi/lo split exact to 22 bits either way
+    # hi/lo split exact to 22 bits either way. Slice maxima of 2^118 and more (x near 1e36)
+    # need the 2^(24 - e) undo factor applied in two parts; the batch then agrees with the
+    # vector-ALU kernel's B = 1 results instead of turning into inf or NaN.
+    scales = np.array([1e30, 1e-30, 1.0, 3e4, 1e-6, 1e36, 5e35], np.float32)
+    B = len(scales)
     xs = S.activations_f32(4242, B * cols).reshape(B, cols)
-    scales = np.array([1e30, 1e-30, 1.0, 3e4, 1e-6], np.float32)
     xr = (xs * scales[:, None]).astype(np.float32)
     xb = backend.upload(xr, shape=(B, cols))
     y = backend.quant_matvec(w, xb)
     got = backend.download(y).reshape(B, rows)
+    assert np.isfinite(got).all()
     for b in range(B):
         assert rel_err(got[b], oracle.matvec_f64(qt.id, blob, rows, cols, xr[b])) <= 1e-5, f"scale {scales[b]}"
+        x1 = backend.upload(xr[b])
+        y1 = backend.quant_matvec(w, x1)
+        assert rel_err(got[b], backend.download(y1).astype(np.float64)) <= 1e-5, f"B=1 vs batch, scale {scales[b]}"
+        backend.release(y1)
+        backend.release(x1)
     backend.release(y)
     backend.release(xb)
 
@@ -430,3 +439,60 @@ def test_concat_rows_fused_gemv(backend, qt, B):
     with pytest.raises(IllegalArgumentException):
         other = backend.upload_quantized(S.quant_blocks(QuantType.Q4_0, 5, 8, cols), QuantType.Q4_0, (8, cols))
         backend.concat_rows([parts[0], other])
+
+
+# K of any block-aligned width (CpuQ4Gemm.java:26-46,79-83; CpuBackend.java:712-714): up to
+# 32768 columns one vector-ALU launch holds x in LDS (15360 was the previous image size,
+# 15488 the first K past it); wider K runs as equal column windows chained through the
+# previous window's y (40960 = two windows of 20480, 53248 = two of 26624). B >= 3 runs the
+# matrix-core kernel in 4096-column windows.
+WIDEK_CASES = [
+    (QuantType.Q4_0, 96, 15360), (QuantType.Q4_0, 96, 15488), (QuantType.Q4_0, 80, 28672),
+    (QuantType.Q8_0, 64, 32768), (QuantType.Q8_0, 40, 40960),
+    (QuantType.Q4_K, 72, 28672), (QuantType.Q4_K, 40, 53248),
+    (QuantType.Q6_K, 64, 32768), (QuantType.Q6_K, 40, 40960),
+    (QuantType.Q2_0, 48, 28672), (QuantType.Q2_0, 24, 40960),
+]
+
+
+@pytest.mark.parametrize("qt,rows,cols", WIDEK_CASES, ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [1, 2, 3, 16])
+def test_gemv_any_k(backend, uploaded, qt, rows, cols, B):
+    if B >= 3 and qt == QuantType.Q2_0:
+        B = 4  # Q2_0 has no matrix-core path: 4 vector-ALU passes
+    note("any-k", qt.name, rows, cols, "B", B)
+    blob, w = uploaded(qt, rows, cols)
+    xs = S.activations_f32(cols + 17 * B, B * cols).reshape(B, cols)
+    add = S.activations_f32(cols + 19, B * rows).reshape(B, rows)
+    xb = backend.upload(xs if B > 1 else xs[0], shape=(B, cols) if B > 1 else None)
+    ab = backend.upload(add if B > 1 else add[0], shape=(B, rows) if B > 1 else None)
+    y = backend.quant_matvec(w, xb)
+    ya = backend.quant_matvec_add(w, xb, ab)
+    got = backend.download(y).reshape(B, rows)
+    gota = backend.download(ya).reshape(B, rows)
+    ref = oracle.matmul_f64(qt.id, blob, rows, cols, xs)
+    # fp32 accumulation over one launch or several chained windows: 1e-5 (the vector-ALU
+    # kernel) and 1e-4 for the matrix-core kernel, whose block sums round one way (the bias
+    # grows with the number of blocks; both far inside the 1e-3 decode tolerance)
+    bound = 1e-5 if B < 3 or qt == QuantType.Q2_0 else 1e-4
+    for b in range(B):
+        assert rel_err(got[b], ref[b]) <= bound, f"row {b}"
+    # the caller's add joins only after the last window, rounded on its own
+    assert np.array_equal(bits(gota), bits(got + add))
+    for h in (xb, ab, y, ya):
+        backend.release(h)
+
+
+def test_in_place_add_wider_than_one_window_is_rejected(backend, uploaded):
+    """An add that overlaps y is read after the first window rewrote y, so above 32768 columns
+    the stream-ordered entry point refuses it (the SPI's quantMatvecAdd always returns a new
+    buffer and is not affected)."""
+    qt, rows, cols = QuantType.Q4_0, 24, 40960
+    blob, w = uploaded(qt, rows, cols)
+    x = backend.upload(S.activations_f32(5, cols))
+    res = backend.upload(np.zeros(rows, np.float32))
+    rp = backend.buffer_desc(res).device_ptr
+    with pytest.raises(IllegalArgumentException, match="overlaps y"):
+        backend.quant_matvec_into(w, backend.buffer_desc(x).device_ptr, rp, rp, 1)
+    backend.release(x)
+    backend.release(res)
