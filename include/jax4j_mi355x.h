@@ -178,6 +178,56 @@ int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *a
 int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, int8_t *xq_dev,
                           float *xs_dev, float *y_dev, void *stream);
 
+/* ---- decode-step plan (engine-local: QuantizedOps.quantMatvec / quantMatvecAdd,
+ *      spi/QuantizedOps.java:27-30, composed over the layers of a decoder step) ---------- */
+/* The quantized matmuls of an n-layer decode step, built once and replayed as one captured
+ * HIP graph. Per layer, on the residual stream h [batch, d_model]:
+ *     qkv[l]     = [q|k|v] . h          gate_up[l] = [gate|up] . h'
+ *     h'         = o . x_o + h          h          = down . x_down + h'
+ * and finally logits = head . h (each "+" a quantMatvecAdd: the add rounded on its own,
+ * CpuBackend.java:728-736). x_o and x_down are the caller's activations (in a full model
+ * the attention output and act(gate) * up, which this path does not compute). q|k|v and
+ * gate|up run as one launch each when their parts share a quant type (the plan holds
+ * row-concatenated copies, see j4q_concat_rows); otherwise as one launch per run of equal
+ * types, with outputs in the same [batch][q|k|v] layout. Every layer must have the same
+ * shapes; quant types may differ. The matrices must stay alive until the plan is
+ * destroyed. The io pointers are bound at creation (the graph records them). */
+typedef uint64_t j4q_plan; /* 0 is never a valid handle */
+
+typedef struct j4q_decode_layer {
+    j4q_buffer q, k, v;   /* [q_rows | kv_rows | kv_rows, d_model] */
+    j4q_buffer o;         /* [d_model, o_cols] */
+    j4q_buffer gate, up;  /* [ffn, d_model] */
+    j4q_buffer down;      /* [d_model, ffn] */
+} j4q_decode_layer;
+
+typedef struct j4q_decode_io {
+    float *h;             /* [batch, d_model] residual stream, read and updated in place (16-byte aligned) */
+    const float *x_o;     /* [batch, o_cols] input of every layer's o (16-byte aligned) */
+    const float *x_down;  /* [batch, ffn] input of every layer's down (16-byte aligned) */
+    float *qkv;           /* [layers][batch][q_rows + 2 kv_rows] */
+    float *gate_up;       /* [layers][batch][2 ffn] */
+    float *logits;        /* [batch, vocab]; may be NULL when there is no head */
+} j4q_decode_io;
+
+typedef struct j4q_decode_plan_desc {
+    int32_t layers;
+    int32_t graph;          /* 1: one step replays as one captured HIP graph */
+    int64_t batch, d_model, qkv_rows, o_cols, ffn, vocab;
+    int64_t gemvs_per_step; /* quantized GEMV calls per step (a fused group counts once) */
+    uint64_t weight_bytes;  /* GGUF bytes of every matrix one step streams */
+    uint64_t plan_bytes;    /* device memory the plan owns (fused copies, residual buffer) */
+} j4q_decode_plan_desc;
+
+/* head may be 0 (no output head). batch in [1, 65535]. */
+int j4q_decode_plan_create(const j4q_decode_layer *layers, int32_t n_layers, j4q_buffer head, int64_t batch,
+                           const j4q_decode_io *io, j4q_plan *out);
+/* Enqueues one step on `stream` (NULL = the engine stream); does not synchronise. */
+int j4q_decode_plan_run(j4q_plan plan, void *stream);
+int j4q_decode_plan_info(j4q_plan plan, j4q_decode_plan_desc *out);
+/* Waits for the device, then frees the graph and the plan's own buffers. 0 is a no-op. */
+int j4q_decode_plan_destroy(j4q_plan plan);
+
 /* ---- GGUF files (the step before uploadQuantized; engine-local) ---------------------- */
 /* The reference receives quantized blobs from an external caller (spi/QuantizedOps.java:24)
  * and knows the GGUF type ids (core/tensor/QuantType.java:3-13); this reader supplies them
@@ -242,6 +292,12 @@ int j4q_spin(uint32_t microseconds, void *stream);
 /* Streaming copy of `nbytes` (a multiple of 16; both pointers 16-byte aligned) with 128-bit
  * loads and stores: a kernel of known traffic, used to scale HBM byte counters. */
 int j4q_copy(void *device_dst, const void *device_src, uint64_t nbytes, void *stream);
+/* Reads `nbytes` (a multiple of 16 below 2 GiB, src 16-byte aligned) once with 128-bit
+ * non-temporal loads, each wave one contiguous segment, and writes nothing but, in a case no
+ * input produces in practice, one word per workgroup to `sink` (workgroups_per_cu x CUs
+ * words): the practical HBM read ceiling of a single launch of that size, against which the
+ * GEMV launches are measured. 1..4 workgroups of 512 threads per CU. */
+int j4q_stream_read(const void *device_src, uint64_t nbytes, uint32_t *sink, int32_t workgroups_per_cu, void *stream);
 
 #ifdef __cplusplus
 }

@@ -76,6 +76,30 @@ class GgufTensor(C.Structure):
     ]
 
 
+class DecodeLayer(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("q", "k", "v", "o", "gate", "up", "down")]
+
+
+class DecodeIO(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("h", "x_o", "x_down", "qkv", "gate_up", "logits")]
+
+
+class DecodePlanDesc(C.Structure):
+    _fields_ = [
+        ("layers", C.c_int32),
+        ("graph", C.c_int32),
+        ("batch", C.c_int64),
+        ("d_model", C.c_int64),
+        ("qkv_rows", C.c_int64),
+        ("o_cols", C.c_int64),
+        ("ffn", C.c_int64),
+        ("vocab", C.c_int64),
+        ("gemvs_per_step", C.c_int64),
+        ("weight_bytes", C.c_uint64),
+        ("plan_bytes", C.c_uint64),
+    ]
+
+
 _i32, _i64, _u64, _vp = C.c_int32, C.c_int64, C.c_uint64, C.c_void_p
 _buf = C.c_uint64
 _pbuf = C.POINTER(C.c_uint64)
@@ -117,6 +141,10 @@ SIGNATURES = {
     "j4q_synth_bf16_host": [_u64, _i64, _vp],
     "j4q_synth_f32_device": [_u64, _i64, _vp, _vp],
     "j4q_synth_bf16_device": [_u64, _i64, _vp, _vp],
+    "j4q_decode_plan_create": [C.POINTER(DecodeLayer), _i32, _buf, _i64, C.POINTER(DecodeIO), C.POINTER(_u64)],
+    "j4q_decode_plan_run": [_u64, _vp],
+    "j4q_decode_plan_info": [_u64, C.POINTER(DecodePlanDesc)],
+    "j4q_decode_plan_destroy": [_u64],
     "j4q_gguf_open": [C.c_char_p, C.POINTER(_u64)],
     "j4q_gguf_close": [_u64],
     "j4q_gguf_file_info": [_u64, C.POINTER(GgufInfo)],
@@ -129,6 +157,7 @@ SIGNATURES = {
     "j4q_gguf_upload": [_u64, _i64, _pbuf],
     "j4q_spin": [C.c_uint32, _vp],
     "j4q_copy": [_vp, _vp, _u64, _vp],
+    "j4q_stream_read": [_vp, _u64, _vp, _i32, _vp],
 }
 _RESTYPES = {"j4q_last_error": C.c_char_p}
 

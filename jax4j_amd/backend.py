@@ -270,6 +270,27 @@ class Mi355xBackend:
             "quantMatmul_into",
         )
 
+    def decode_plan(self, layers, head, batch: int, io: dict) -> "DecodePlan":
+        """The quantized matmuls of a decode step as one replayable plan (engine-local).
+
+        ``layers``: per layer a dict of quantized buffers q, k, v, o, gate, up, down; ``head``:
+        the output head or None; ``io``: device pointers h (residual stream, updated in place),
+        x_o, x_down (inputs of o and down), qkv, gate_up (per-layer outputs) and logits.
+        Per layer: qkv = [q|k|v].h; h' = o.x_o + h; gate_up = [gate|up].h'; h = down.x_down + h';
+        finally logits = head.h.
+        """
+        arr = (N.DecodeLayer * len(layers))()
+        for i, l in enumerate(layers):
+            for k in ("q", "k", "v", "o", "gate", "up", "down"):
+                setattr(arr[i], k, l[k].handle)
+        cio = N.DecodeIO(**{k: C.c_void_p(io.get(k) or None) for k in ("h", "x_o", "x_down", "qkv", "gate_up", "logits")})
+        out = C.c_uint64()
+        check(
+            self._lib().j4q_decode_plan_create(arr, len(layers), head.handle if head else 0, batch, C.byref(cio), C.byref(out)),
+            "decode plan",
+        )
+        return DecodePlan(self, out.value)
+
     # ---- helpers ---------------------------------------------------------------------------
     def _check_device(self, device: Device | None) -> None:
         if device is not None and (device.type != DeviceType.ROCM or device.index != self._device):
@@ -282,6 +303,27 @@ class Mi355xBackend:
         else:
             shape = (x.shape[0], rows)
         return DeviceBuffer(handle, shape, DType.F32, weights.device)
+
+
+class DecodePlan:
+    """A decode step built once by ``Mi355xBackend.decode_plan`` (one captured HIP graph)."""
+
+    def __init__(self, backend: Mi355xBackend, handle: int):
+        self._be = backend
+        self.handle = handle
+
+    def run(self, stream: int = 0) -> None:
+        """Enqueue one step on ``stream`` (0 = the engine stream); no synchronisation."""
+        check(self._be._lib().j4q_decode_plan_run(self.handle, C.c_void_p(stream or None)), "decode plan run")
+
+    def info(self) -> dict:
+        d = N.DecodePlanDesc()
+        check(self._be._lib().j4q_decode_plan_info(self.handle, C.byref(d)), "decode plan info")
+        return {name: getattr(d, name) for name, _ in N.DecodePlanDesc._fields_}
+
+    def destroy(self) -> None:
+        check(self._be._lib().j4q_decode_plan_destroy(self.handle), "decode plan destroy")
+        self.handle = 0
 
 
 _DEFAULT: Mi355xBackend | None = None

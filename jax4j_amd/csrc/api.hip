@@ -9,8 +9,7 @@
 #include <string>
 #include <vector>
 
-#include "j4q_common.h"
-#include "jax4j_mi355x.h"
+#include "engine.h"
 #include "synth.h"
 
 namespace j4q {
@@ -51,10 +50,7 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
-int hip_fail(const char *op, hipError_t e) {
-    const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? J4Q_ENOMEM : J4Q_EHIP;
-    return fail(code, "%s failed: %s (code %d)", op, hipGetErrorString(e), (int)e);
-}
+int hip_fail(const char *op, hipError_t e) { return j4q::report_hip(op, e); }
 
 #define HIP_TRY(op, expr)                         \
     do {                                          \
@@ -65,8 +61,8 @@ int hip_fail(const char *op, hipError_t e) {
 }  // namespace
 
 namespace j4q {
-// Error reporting for the GGUF reader (gguf.hip): same thread-local message as every entry point.
-int gguf_fail(int code, const char *fmt, ...) {
+// Error reporting for the other translation units: same thread-local message as every entry point.
+int report_error(int code, const char *fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -74,6 +70,11 @@ int gguf_fail(int code, const char *fmt, ...) {
     va_end(ap);
     t_err = buf;
     return code;
+}
+
+int report_hip(const char *op, hipError_t e) {
+    const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? J4Q_ENOMEM : J4Q_EHIP;
+    return report_error(code, "%s failed: %s (code %d)", op, hipGetErrorString(e), (int)e);
 }
 }  // namespace j4q
 
@@ -341,6 +342,83 @@ hipStream_t pick_stream(void *s) { return s ? (hipStream_t)s : g_stream; }
 
 }  // namespace
 
+namespace j4q {
+namespace abi {
+
+std::mutex &lock() { return g_mu; }
+int ready_locked() { return ensure_ready(); }
+hipStream_t stream() { return g_stream; }
+
+int quant_locked(j4q_buffer h, const char *op, QuantRef *out) {
+    Buf *b;
+    const int rc = get_buf(h, J4Q_KIND_QUANT, op, &b);
+    if (rc) return rc;
+    Geometry g;
+    geometry_of(b->qtype, &g);
+    out->qtype = b->qtype;
+    out->rows = b->dims[0];
+    out->cols = b->dims[1];
+    out->m = qmat_of(*b);
+    out->gguf_bytes = (uint64_t)(b->dims[0] * (b->dims[1] / g.block_elements)) * (uint64_t)g.block_bytes;
+    return J4Q_OK;
+}
+
+int concat_locked(const j4q_buffer *parts, int count, void **dev_out, QuantRef *out) {
+    if (count < 1 || count > 64) return fail(J4Q_EINVAL, "concat_rows: count %d out of range [1, 64]", count);
+    int rc;
+    std::vector<Buf *> ps((size_t)count);
+    int64_t rows = 0;
+    for (int i = 0; i < count; i++) {
+        if ((rc = get_buf(parts[i], J4Q_KIND_QUANT, "concat_rows", &ps[(size_t)i]))) return rc;
+        if (ps[(size_t)i]->qtype != ps[0]->qtype || ps[(size_t)i]->dims[1] != ps[0]->dims[1])
+            return fail(J4Q_EINVAL, "concat_rows: part %d is type %d with %lld columns; part 0 is type %d with %lld", i,
+                        ps[(size_t)i]->qtype, (long long)ps[(size_t)i]->dims[1], ps[0]->qtype, (long long)ps[0]->dims[1]);
+        rows += ps[(size_t)i]->dims[0];
+    }
+    const int qt = ps[0]->qtype;
+    const int64_t cols = ps[0]->dims[1];
+    if ((rc = check_sections(qt, rows, cols))) return rc;
+    if ((rc = ensure_ready())) return rc;
+    // every row-major section of the split layout lands at the part's row offset in the
+    // matching section of the result; Q8_0's block-major scale copy is rebuilt afterwards
+    const SplitLayout L = split_layout(qt, rows, cols);
+    void *dev = nullptr;
+    HIP_TRY("hipMalloc", hipMalloc(&dev, L.total));
+    hipError_t e = hipSuccess;
+    uint64_t off[4] = {0, 0, 0, 0};
+    for (int i = 0; i < count && e == hipSuccess; i++) {
+        const Buf &b = *ps[(size_t)i];
+        const SplitLayout P = split_layout(qt, b.dims[0], cols);
+        const uint64_t src_off[4] = {P.qs_off, P.qh_off, P.sc_off, P.d_off};
+        const uint64_t dst_off[4] = {L.qs_off, L.qh_off, L.sc_off, L.d_off};
+        const uint64_t len[4] = {P.qs_bytes, P.qh_bytes, P.sc_bytes, qt == Q8_0 ? 0 : P.d_bytes};
+        for (int sct = 0; sct < 4 && e == hipSuccess; sct++) {
+            if (!len[sct]) continue;
+            e = hipMemcpyAsync((uint8_t *)dev + dst_off[sct] + off[sct], (const uint8_t *)b.dev + src_off[sct], len[sct],
+                               hipMemcpyDeviceToDevice, g_stream);
+            off[sct] += len[sct];
+        }
+    }
+    if (e == hipSuccess && qt == Q8_0) e = launch_q8_scales_t(qmat_view((const uint8_t *)dev, qt, rows, cols), g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail("concat_rows", e);
+    }
+    Geometry g;
+    geometry_of(qt, &g);
+    out->qtype = qt;
+    out->rows = rows;
+    out->cols = cols;
+    out->m = qmat_view((const uint8_t *)dev, qt, rows, cols);
+    out->gguf_bytes = (uint64_t)(rows * (cols / g.block_elements)) * (uint64_t)g.block_bytes;
+    *dev_out = dev;
+    return J4Q_OK;
+}
+
+}  // namespace abi
+}  // namespace j4q
+
 extern "C" {
 
 int j4q_abi_version(void) { return J4Q_ABI_VERSION; }
@@ -459,56 +537,19 @@ int j4q_export_quantized(j4q_buffer wh, void *blocks, uint64_t nbytes) {
 
 int j4q_concat_rows(const j4q_buffer *parts, int32_t count, j4q_buffer *out) {
     if (!parts || !out) return fail(J4Q_EINVAL, "concat_rows: NULL argument");
-    if (count < 1 || count > 64) return fail(J4Q_EINVAL, "concat_rows: count %d out of range [1, 64]", count);
     std::lock_guard<std::mutex> lk(g_mu);
-    int rc;
-    std::vector<Buf *> ps((size_t)count);
-    int64_t rows = 0;
-    for (int i = 0; i < count; i++) {
-        if ((rc = get_buf(parts[i], J4Q_KIND_QUANT, "concat_rows", &ps[(size_t)i]))) return rc;
-        if (ps[(size_t)i]->qtype != ps[0]->qtype || ps[(size_t)i]->dims[1] != ps[0]->dims[1])
-            return fail(J4Q_EINVAL, "concat_rows: part %d is type %d with %lld columns; part 0 is type %d with %lld", i,
-                        ps[(size_t)i]->qtype, (long long)ps[(size_t)i]->dims[1], ps[0]->qtype, (long long)ps[0]->dims[1]);
-        rows += ps[(size_t)i]->dims[0];
-    }
-    const int qt = ps[0]->qtype;
-    const int64_t cols = ps[0]->dims[1];
-    if ((rc = check_sections(qt, rows, cols))) return rc;
-    if ((rc = ensure_ready())) return rc;
-    // every row-major section of the split layout lands at the part's row offset in the
-    // matching section of the result; Q8_0's block-major scale copy is rebuilt afterwards
-    const j4q::SplitLayout L = j4q::split_layout(qt, rows, cols);
     void *dev = nullptr;
-    HIP_TRY("hipMalloc", hipMalloc(&dev, L.total));
-    hipError_t e = hipSuccess;
-    uint64_t off[4] = {0, 0, 0, 0};
-    for (int i = 0; i < count && e == hipSuccess; i++) {
-        const Buf &b = *ps[(size_t)i];
-        const j4q::SplitLayout P = j4q::split_layout(qt, b.dims[0], cols);
-        const uint64_t src_off[4] = {P.qs_off, P.qh_off, P.sc_off, P.d_off};
-        const uint64_t dst_off[4] = {L.qs_off, L.qh_off, L.sc_off, L.d_off};
-        const uint64_t len[4] = {P.qs_bytes, P.qh_bytes, P.sc_bytes, qt == j4q::Q8_0 ? 0 : P.d_bytes};
-        for (int sct = 0; sct < 4 && e == hipSuccess; sct++) {
-            if (!len[sct]) continue;
-            e = hipMemcpyAsync((uint8_t *)dev + dst_off[sct] + off[sct], (const uint8_t *)b.dev + src_off[sct], len[sct],
-                               hipMemcpyDeviceToDevice, g_stream);
-            off[sct] += len[sct];
-        }
-    }
-    if (e == hipSuccess && qt == j4q::Q8_0) e = j4q::launch_q8_scales_t(j4q::qmat_view((const uint8_t *)dev, qt, rows, cols), g_stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
-    if (e != hipSuccess) {
-        (void)hipFree(dev);
-        return hip_fail("concat_rows", e);
-    }
+    j4q::abi::QuantRef r;
+    int rc = j4q::abi::concat_locked(parts, count, &dev, &r);
+    if (rc) return rc;
     Buf nb;
     nb.kind = J4Q_KIND_QUANT;
-    nb.qtype = qt;
+    nb.qtype = r.qtype;
     nb.rank = 2;
-    nb.dims[0] = rows;
-    nb.dims[1] = cols;
+    nb.dims[0] = r.rows;
+    nb.dims[1] = r.cols;
     nb.dev = dev;
-    nb.bytes = L.total;
+    nb.bytes = j4q::split_layout(r.qtype, r.rows, r.cols).total;
     *out = register_buf(nb);
     return J4Q_OK;
 }
@@ -805,6 +846,20 @@ int j4q_spin(uint32_t microseconds, void *stream) {
     int khz = 0;
     HIP_TRY("hipDeviceGetAttribute", hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, g_dev));
     HIP_TRY("spin", j4q::launch_spin(microseconds, khz, pick_stream(stream)));
+    return J4Q_OK;
+}
+
+int j4q_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int32_t workgroups_per_cu, void *stream) {
+    if (!src || !sink) return fail(J4Q_EINVAL, "stream_read: NULL pointer");
+    if (nbytes % 16 != 0 || !aligned(src, 16) || nbytes >= 0x80000000ull)
+        return fail(J4Q_EINVAL, "stream_read: nbytes must be a multiple of 16 below 2 GiB, src 16-byte aligned");
+    if (workgroups_per_cu < 1 || workgroups_per_cu > 4) return fail(J4Q_EINVAL, "stream_read: workgroups_per_cu %d out of range [1, 4]", workgroups_per_cu);
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = ensure_ready();
+    if (rc) return rc;
+    hipDeviceProp_t p;
+    HIP_TRY("hipGetDeviceProperties", hipGetDeviceProperties(&p, g_dev));
+    HIP_TRY("stream_read", j4q::launch_stream_read(src, nbytes, sink, workgroups_per_cu * p.multiProcessorCount, pick_stream(stream)));
     return J4Q_OK;
 }
 

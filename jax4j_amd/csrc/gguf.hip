@@ -27,12 +27,7 @@
 #include <unordered_map>
 #include <vector>
 
-#include "j4q_common.h"
-#include "jax4j_mi355x.h"
-
-namespace j4q {
-int gguf_fail(int code, const char *fmt, ...);
-}
+#include "engine.h"
 
 namespace {
 
@@ -115,13 +110,13 @@ class Reader {
     bool need(uint64_t k) const { return k <= n_ && off_ <= n_ - k; }
     template <typename T>
     int get(T *v, const char *what) {
-        if (!need(sizeof(T))) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: truncated reading %s at byte %llu", what, (unsigned long long)off_);
+        if (!need(sizeof(T))) return j4q::report_error(J4Q_EINVAL, "GGUF: truncated reading %s at byte %llu", what, (unsigned long long)off_);
         memcpy(v, p_ + off_, sizeof(T));
         off_ += sizeof(T);
         return J4Q_OK;
     }
     int skip(uint64_t k, const char *what) {
-        if (!need(k)) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: truncated %s at byte %llu", what, (unsigned long long)off_);
+        if (!need(k)) return j4q::report_error(J4Q_EINVAL, "GGUF: truncated %s at byte %llu", what, (unsigned long long)off_);
         off_ += k;
         return J4Q_OK;
     }
@@ -130,7 +125,7 @@ class Reader {
         int rc = get(&len, what);
         if (rc) return rc;
         if (len > (1u << 20) || !need(len))
-            return j4q::gguf_fail(J4Q_EINVAL, "GGUF: %s string of %llu bytes at byte %llu exceeds the file", what,
+            return j4q::report_error(J4Q_EINVAL, "GGUF: %s string of %llu bytes at byte %llu exceeds the file", what,
                                   (unsigned long long)len, (unsigned long long)off_);
         s->assign(reinterpret_cast<const char *>(p_ + off_), len);
         off_ += len;
@@ -144,7 +139,7 @@ class Reader {
 
 // Skips one metadata value of type t (arrays of arrays included, depth-limited).
 int skip_value(Reader &r, uint32_t t, int depth) {
-    if (depth > 4) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: arrays nested too deeply at byte %llu", (unsigned long long)r.pos());
+    if (depth > 4) return j4q::report_error(J4Q_EINVAL, "GGUF: arrays nested too deeply at byte %llu", (unsigned long long)r.pos());
     if (const int sz = scalar_size(t)) return r.skip((uint64_t)sz, "metadata value");
     if (t == T_STRING) {
         std::string s;
@@ -157,14 +152,14 @@ int skip_value(Reader &r, uint32_t t, int depth) {
         if (!rc) rc = r.get(&cnt, "array count");
         if (rc) return rc;
         if (const int sz = scalar_size(et)) {
-            if (cnt > (uint64_t)1 << 40) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: array of %llu elements", (unsigned long long)cnt);
+            if (cnt > (uint64_t)1 << 40) return j4q::report_error(J4Q_EINVAL, "GGUF: array of %llu elements", (unsigned long long)cnt);
             return r.skip(cnt * (uint64_t)sz, "array");
         }
         for (uint64_t i = 0; i < cnt; i++)
             if ((rc = skip_value(r, et, depth + 1))) return rc;
         return J4Q_OK;
     }
-    return j4q::gguf_fail(J4Q_EINVAL, "GGUF: unknown metadata value type %u at byte %llu", t, (unsigned long long)r.pos());
+    return j4q::report_error(J4Q_EINVAL, "GGUF: unknown metadata value type %u at byte %llu", t, (unsigned long long)r.pos());
 }
 
 int parse(File *f) {
@@ -172,15 +167,15 @@ int parse(File *f) {
     uint32_t magic;
     int rc = r.get(&magic, "magic");
     if (rc) return rc;
-    if (magic != 0x46554747u) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: bad magic 0x%08x (not a GGUF file)", magic);
+    if (magic != 0x46554747u) return j4q::report_error(J4Q_EINVAL, "GGUF: bad magic 0x%08x (not a GGUF file)", magic);
     if ((rc = r.get(&f->version, "version"))) return rc;
     if (f->version != 2 && f->version != 3)
-        return j4q::gguf_fail(J4Q_EUNSUPPORTED, "GGUF: version %u not supported (2 or 3)", f->version);
+        return j4q::report_error(J4Q_EUNSUPPORTED, "GGUF: version %u not supported (2 or 3)", f->version);
     uint64_t nt, nkv;
     if ((rc = r.get(&nt, "tensor count")) || (rc = r.get(&nkv, "metadata count"))) return rc;
     // every entry takes more than 8 bytes, so larger counts cannot fit the file
     if (nt > f->size / 8 || nkv > f->size / 8)
-        return j4q::gguf_fail(J4Q_EINVAL, "GGUF: %llu tensors / %llu metadata entries cannot fit %llu bytes",
+        return j4q::report_error(J4Q_EINVAL, "GGUF: %llu tensors / %llu metadata entries cannot fit %llu bytes",
                               (unsigned long long)nt, (unsigned long long)nkv, (unsigned long long)f->size);
     for (uint64_t i = 0; i < nkv; i++) {
         Meta m;
@@ -195,10 +190,10 @@ int parse(File *f) {
         }
         if ((rc = skip_value(r, m.type, 0))) return rc;
         if (m.key == "general.alignment") {
-            if (m.type != T_U32) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: general.alignment has type %u, not u32", m.type);
+            if (m.type != T_U32) return j4q::report_error(J4Q_EINVAL, "GGUF: general.alignment has type %u, not u32", m.type);
             uint32_t a;
             memcpy(&a, f->map + m.pos, 4);
-            if (a == 0 || (a & (a - 1)) != 0) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: general.alignment %u is not a power of two", a);
+            if (a == 0 || (a & (a - 1)) != 0) return j4q::report_error(J4Q_EINVAL, "GGUF: general.alignment %u is not a power of two", a);
             f->alignment = a;
         }
         f->meta.push_back(std::move(m));
@@ -207,12 +202,12 @@ int parse(File *f) {
         Tensor t;
         if ((rc = r.str(&t.name, "tensor name")) || (rc = r.get(&t.n_dims, "tensor n_dims"))) return rc;
         if (t.n_dims == 0 || t.n_dims > 4)
-            return j4q::gguf_fail(J4Q_EINVAL, "GGUF: tensor '%s' has %u dimensions (1..4)", t.name.c_str(), t.n_dims);
+            return j4q::report_error(J4Q_EINVAL, "GGUF: tensor '%s' has %u dimensions (1..4)", t.name.c_str(), t.n_dims);
         uint64_t elems = 1;
         for (uint32_t d = 0; d < t.n_dims; d++) {
             if ((rc = r.get(&t.dims[d], "tensor dims"))) return rc;
             if (t.dims[d] == 0 || t.dims[d] > ((uint64_t)1 << 40) || elems > ((uint64_t)1 << 62) / t.dims[d])
-                return j4q::gguf_fail(J4Q_EINVAL, "GGUF: tensor '%s' dimension %u = %llu out of range", t.name.c_str(), d,
+                return j4q::report_error(J4Q_EINVAL, "GGUF: tensor '%s' dimension %u = %llu out of range", t.name.c_str(), d,
                                       (unsigned long long)t.dims[d]);
             elems *= t.dims[d];
         }
@@ -220,11 +215,11 @@ int parse(File *f) {
         int be, bb;
         if (ggml_geometry(t.type, &be, &bb)) {
             if (t.dims[0] % (uint64_t)be != 0)
-                return j4q::gguf_fail(J4Q_EINVAL, "GGUF: tensor '%s' row of %llu elements is not a multiple of its block (%d)",
+                return j4q::report_error(J4Q_EINVAL, "GGUF: tensor '%s' row of %llu elements is not a multiple of its block (%d)",
                                       t.name.c_str(), (unsigned long long)t.dims[0], be);
             t.nbytes = elems / (uint64_t)be * (uint64_t)bb;
         }
-        if (f->by_name.count(t.name)) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: duplicate tensor name '%s'", t.name.c_str());
+        if (f->by_name.count(t.name)) return j4q::report_error(J4Q_EINVAL, "GGUF: duplicate tensor name '%s'", t.name.c_str());
         f->by_name[t.name] = f->tensors.size();
         f->tensors.push_back(std::move(t));
     }
@@ -232,10 +227,10 @@ int parse(File *f) {
     f->data_offset = (end + f->alignment - 1) / f->alignment * f->alignment;
     for (Tensor &t : f->tensors) {
         if (t.offset % f->alignment != 0)
-            return j4q::gguf_fail(J4Q_EINVAL, "GGUF: tensor '%s' offset %llu is not a multiple of the alignment %llu",
+            return j4q::report_error(J4Q_EINVAL, "GGUF: tensor '%s' offset %llu is not a multiple of the alignment %llu",
                                   t.name.c_str(), (unsigned long long)t.offset, (unsigned long long)f->alignment);
         if (t.offset > f->size || f->data_offset > f->size - t.offset || t.nbytes > f->size - f->data_offset - t.offset)
-            return j4q::gguf_fail(J4Q_EINVAL, "GGUF: tensor '%s' (%llu bytes at data offset %llu) extends past the end of the file (%llu bytes)",
+            return j4q::report_error(J4Q_EINVAL, "GGUF: tensor '%s' (%llu bytes at data offset %llu) extends past the end of the file (%llu bytes)",
                                   t.name.c_str(), (unsigned long long)t.nbytes, (unsigned long long)t.offset, (unsigned long long)f->size);
         t.offset += f->data_offset;
     }
@@ -250,24 +245,24 @@ File *file_of(j4q_gguf h) {
 
 int get_file(j4q_gguf h, File **f) {
     *f = file_of(h);
-    return *f ? J4Q_OK : j4q::gguf_fail(J4Q_EHANDLE, "GGUF: unknown or closed file handle %llu", (unsigned long long)h);
+    return *f ? J4Q_OK : j4q::report_error(J4Q_EHANDLE, "GGUF: unknown or closed file handle %llu", (unsigned long long)h);
 }
 
 int get_tensor(File *f, int64_t index, Tensor **t) {
     if (index < 0 || (uint64_t)index >= f->tensors.size())
-        return j4q::gguf_fail(J4Q_EINVAL, "GGUF: tensor index %lld out of range [0, %zu)", (long long)index, f->tensors.size());
+        return j4q::report_error(J4Q_EINVAL, "GGUF: tensor index %lld out of range [0, %zu)", (long long)index, f->tensors.size());
     *t = &f->tensors[(size_t)index];
     return J4Q_OK;
 }
 
 int get_meta(File *f, const char *key, Meta **m) {
-    if (!key) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: key is NULL");
+    if (!key) return j4q::report_error(J4Q_EINVAL, "GGUF: key is NULL");
     for (Meta &e : f->meta)
         if (e.key == key) {
             *m = &e;
             return J4Q_OK;
         }
-    return j4q::gguf_fail(J4Q_EINVAL, "GGUF: no metadata key '%s'", key);
+    return j4q::report_error(J4Q_EINVAL, "GGUF: no metadata key '%s'", key);
 }
 
 void copy_cstr(char *dst, size_t cap, const std::string &s) {
@@ -282,18 +277,18 @@ void copy_cstr(char *dst, size_t cap, const std::string &s) {
 extern "C" {
 
 int j4q_gguf_open(const char *path, j4q_gguf *out) {
-    if (!path || !out) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: NULL argument");
+    if (!path || !out) return j4q::report_error(J4Q_EINVAL, "GGUF: NULL argument");
     *out = 0;
     const int fd = open(path, O_RDONLY | O_CLOEXEC);
-    if (fd < 0) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: cannot open '%s': %s", path, strerror(errno));
+    if (fd < 0) return j4q::report_error(J4Q_EINVAL, "GGUF: cannot open '%s': %s", path, strerror(errno));
     struct stat st;
     if (fstat(fd, &st) != 0 || st.st_size <= 0) {
         close(fd);
-        return j4q::gguf_fail(J4Q_EINVAL, "GGUF: '%s' is empty or unreadable", path);
+        return j4q::report_error(J4Q_EINVAL, "GGUF: '%s' is empty or unreadable", path);
     }
     void *map = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
     close(fd);
-    if (map == MAP_FAILED) return j4q::gguf_fail(J4Q_ENOMEM, "GGUF: cannot map '%s': %s", path, strerror(errno));
+    if (map == MAP_FAILED) return j4q::report_error(J4Q_ENOMEM, "GGUF: cannot map '%s': %s", path, strerror(errno));
     File *f = new File;
     f->map = static_cast<const uint8_t *>(map);
     f->size = (uint64_t)st.st_size;
@@ -322,7 +317,7 @@ int j4q_gguf_close(j4q_gguf h) {
 }
 
 int j4q_gguf_file_info(j4q_gguf h, j4q_gguf_info *out) {
-    if (!out) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: out is NULL");
+    if (!out) return j4q::report_error(J4Q_EINVAL, "GGUF: out is NULL");
     std::lock_guard<std::mutex> lk(g_gmu);
     File *f;
     if (int rc = get_file(h, &f)) return rc;
@@ -337,7 +332,7 @@ int j4q_gguf_file_info(j4q_gguf h, j4q_gguf_info *out) {
 }
 
 int j4q_gguf_tensor_info(j4q_gguf h, int64_t index, j4q_gguf_tensor *out) {
-    if (!out) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: out is NULL");
+    if (!out) return j4q::report_error(J4Q_EINVAL, "GGUF: out is NULL");
     std::lock_guard<std::mutex> lk(g_gmu);
     File *f;
     Tensor *t;
@@ -354,12 +349,12 @@ int j4q_gguf_tensor_info(j4q_gguf h, int64_t index, j4q_gguf_tensor *out) {
 }
 
 int j4q_gguf_find_tensor(j4q_gguf h, const char *name, int64_t *index) {
-    if (!name || !index) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: NULL argument");
+    if (!name || !index) return j4q::report_error(J4Q_EINVAL, "GGUF: NULL argument");
     std::lock_guard<std::mutex> lk(g_gmu);
     File *f;
     if (int rc = get_file(h, &f)) return rc;
     const auto it = f->by_name.find(name);
-    if (it == f->by_name.end()) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: no tensor named '%s'", name);
+    if (it == f->by_name.end()) return j4q::report_error(J4Q_EINVAL, "GGUF: no tensor named '%s'", name);
     *index = (int64_t)it->second;
     return J4Q_OK;
 }
@@ -370,7 +365,7 @@ int j4q_gguf_meta_key(j4q_gguf h, int64_t index, char *key, int32_t cap, int32_t
     File *f;
     if (int rc = get_file(h, &f)) return rc;
     if (index < 0 || (uint64_t)index >= f->meta.size())
-        return j4q::gguf_fail(J4Q_EINVAL, "GGUF: metadata index %lld out of range [0, %zu)", (long long)index, f->meta.size());
+        return j4q::report_error(J4Q_EINVAL, "GGUF: metadata index %lld out of range [0, %zu)", (long long)index, f->meta.size());
     const Meta &m = f->meta[(size_t)index];
     if (cap > 0) copy_cstr(key, (size_t)cap, m.key);
     if (type) *type = (int32_t)m.type;
@@ -380,14 +375,14 @@ int j4q_gguf_meta_key(j4q_gguf h, int64_t index, char *key, int32_t cap, int32_t
 }
 
 int j4q_gguf_meta_scalar(j4q_gguf h, const char *key, int32_t *type, void *value8) {
-    if (!value8) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: value is NULL");
+    if (!value8) return j4q::report_error(J4Q_EINVAL, "GGUF: value is NULL");
     std::lock_guard<std::mutex> lk(g_gmu);
     File *f;
     Meta *m;
     if (int rc = get_file(h, &f)) return rc;
     if (int rc = get_meta(f, key, &m)) return rc;
     const int sz = scalar_size(m->type);
-    if (!sz) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: metadata '%s' has type %u, not a scalar", key, m->type);
+    if (!sz) return j4q::report_error(J4Q_EINVAL, "GGUF: metadata '%s' has type %u, not a scalar", key, m->type);
     memset(value8, 0, 8);
     memcpy(value8, f->map + m->pos, (size_t)sz);
     if (type) *type = (int32_t)m->type;
@@ -400,7 +395,7 @@ int j4q_gguf_meta_string(j4q_gguf h, const char *key, char *out, uint64_t cap, u
     Meta *m;
     if (int rc = get_file(h, &f)) return rc;
     if (int rc = get_meta(f, key, &m)) return rc;
-    if (m->type != T_STRING) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: metadata '%s' has type %u, not a string", key, m->type);
+    if (m->type != T_STRING) return j4q::report_error(J4Q_EINVAL, "GGUF: metadata '%s' has type %u, not a string", key, m->type);
     if (length) *length = m->count;
     if (out && cap > 0) {
         const uint64_t n = m->count < cap - 1 ? m->count : cap - 1;
@@ -411,22 +406,22 @@ int j4q_gguf_meta_string(j4q_gguf h, const char *key, char *out, uint64_t cap, u
 }
 
 int j4q_gguf_read_tensor(j4q_gguf h, int64_t index, void *dst, uint64_t nbytes) {
-    if (!dst) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: dst is NULL");
+    if (!dst) return j4q::report_error(J4Q_EINVAL, "GGUF: dst is NULL");
     std::lock_guard<std::mutex> lk(g_gmu);
     File *f;
     Tensor *t;
     if (int rc = get_file(h, &f)) return rc;
     if (int rc = get_tensor(f, index, &t)) return rc;
-    if (t->nbytes == 0) return j4q::gguf_fail(J4Q_EUNSUPPORTED, "GGUF: tensor '%s' has ggml type %u of unknown size", t->name.c_str(), t->type);
+    if (t->nbytes == 0) return j4q::report_error(J4Q_EUNSUPPORTED, "GGUF: tensor '%s' has ggml type %u of unknown size", t->name.c_str(), t->type);
     if (nbytes != t->nbytes)
-        return j4q::gguf_fail(J4Q_EINVAL, "GGUF: tensor '%s' holds %llu bytes, not %llu", t->name.c_str(),
+        return j4q::report_error(J4Q_EINVAL, "GGUF: tensor '%s' holds %llu bytes, not %llu", t->name.c_str(),
                               (unsigned long long)t->nbytes, (unsigned long long)nbytes);
     memcpy(dst, f->map + t->offset, t->nbytes);
     return J4Q_OK;
 }
 
 int j4q_gguf_upload(j4q_gguf h, int64_t index, j4q_buffer *out) {
-    if (!out) return j4q::gguf_fail(J4Q_EINVAL, "GGUF: out is NULL");
+    if (!out) return j4q::report_error(J4Q_EINVAL, "GGUF: out is NULL");
     // The file lock is held through the upload, so a concurrent close cannot unmap the
     // blocks while they are copied (the engine lock is only ever taken after this one).
     std::lock_guard<std::mutex> lk(g_gmu);

@@ -412,6 +412,41 @@ hipError_t launch_copy(void *dst, const void *src, uint64_t nbytes, hipStream_t 
     return hipGetLastError();
 }
 
+// Read-only streaming probe: wave w of the grid reads its own contiguous segment of `seg`
+// bytes (a multiple of 4 KB) with 128-bit non-temporal buffer loads, 1 KB per load
+// instruction and four in flight, and writes nothing but a per-workgroup value no input
+// produces in practice (so the loads cannot be dropped). Offsets past nbytes are out of the
+// buffer resource's range: those loads return zeros without touching memory. It measures
+// the practical HBM read ceiling of one launch of a given size: the same dispatch, ramp and
+// tail a GEMV launch of that many bytes pays.
+__global__ void __launch_bounds__(512) stream_read_kernel(const void *src, uint32_t nbytes, uint32_t seg,
+                                                          uint32_t *__restrict__ sink) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(src), (short)0, (int)nbytes, 0x00020000);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = blockIdx.x * 8u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t base = w * seg + lane * 16u;
+    uint32_t acc = 0;
+    for (uint32_t off = 0; off < seg; off += 4096u) {
+        cu32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            v[u] = __builtin_bit_cast(cu32x4, __builtin_amdgcn_raw_buffer_load_b128(r, base + off + 1024u * u, 0, 2));
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+// nbytes < 2^31 (32-bit buffer offsets; the caller checks).
+hipError_t launch_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int grid, hipStream_t s) {
+    if (nbytes == 0) return hipSuccess;
+    if (nbytes >= 0x80000000ull || grid <= 0) return hipErrorInvalidValue;
+    const uint64_t waves = (uint64_t)grid * 8;
+    const uint64_t seg = (nbytes + waves * 4096 - 1) / (waves * 4096) * 4096;
+    stream_read_kernel<<<(unsigned)grid, 512, 0, s>>>(src, (uint32_t)nbytes, (uint32_t)seg, sink);
+    return hipGetLastError();
+}
+
 hipError_t launch_spin(uint32_t microseconds, int wall_clock_khz, hipStream_t s) {
     const uint64_t ticks = (uint64_t)microseconds * (uint64_t)(wall_clock_khz > 0 ? wall_clock_khz : 100000) / 1000u;
     spin_kernel<<<1, 64, 0, s>>>(ticks);

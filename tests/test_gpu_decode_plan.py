@@ -1,0 +1,222 @@
+"""The decode-step plan (j4q_decode_plan_*): a reduced decoder step against the eager
+composition of quantMatvec / quantMatvecAdd calls and against the CPU oracle.
+
+Per layer the plan computes qkv = [q|k|v].h, h' = o.x_o + h, gate_up = [gate|up].h',
+h = down.x_down + h', then logits = head.h, replayed as one captured HIP graph
+(QuantizedOps.java:27-30; CpuBackend.java:708-736 per GEMV). The plan runs the same kernels
+as the single calls, so its outputs equal the eager composition bit for bit; against the
+fp64 oracle chain the fp32 residual stream adds its roundings, bound 1e-4 * ||ref||_inf
+(10x inside the 1e-3 decode tolerance).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from jax4j_amd import IllegalArgumentException, QuantType
+from jax4j_amd import _native as N
+from jax4j_amd import synthetic as S
+from jax4j_amd.backend import DecodePlan
+
+pytestmark = pytest.mark.gpu
+
+Q4K, Q6K, Q8, Q40 = QuantType.Q4_K, QuantType.Q6_K, QuantType.Q8_0, QuantType.Q4_0
+D, QR, KVR, FFN, VOCAB = 512, 512, 256, 1024, 1000
+# layer 0: one type per group (q|k|v and gate|up fused into one launch each); layer 1: v and
+# up of other types (runs launched separately, outputs copied into the fused layout)
+TYPES = [
+    dict(q=Q4K, k=Q4K, v=Q4K, o=Q4K, gate=Q4K, up=Q4K, down=Q6K),
+    dict(q=Q4K, k=Q4K, v=Q6K, o=Q40, gate=Q4K, up=Q8, down=Q6K),
+]
+SHAPES = dict(q=(QR, D), k=(KVR, D), v=(KVR, D), o=(D, QR), gate=(FFN, D), up=(FFN, D), down=(D, FFN))
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def note(*parts):
+    print("[case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def rel_err(y, y_ref):
+    return float(np.abs(y.astype(np.float64) - y_ref).max() / max(np.abs(y_ref).max(), 1e-30))
+
+
+def ptr(backend, buf):
+    return backend.buffer_desc(buf).device_ptr
+
+
+@pytest.fixture(scope="module")
+def model(backend):
+    """Two layers of weights and a head (host blobs kept for the oracle)."""
+    layers, blobs = [], []
+    seed = 0xD0C
+    for types in TYPES:
+        lw, lb = {}, {}
+        for name, qt in types.items():
+            rows, cols = SHAPES[name]
+            blob = S.quant_blocks(qt, seed, rows, cols)
+            seed += 1
+            lb[name] = (qt, blob)
+            lw[name] = backend.upload_quantized(blob, qt, (rows, cols))
+        layers.append(lw)
+        blobs.append(lb)
+    hblob = S.quant_blocks(Q6K, seed, VOCAB, D)
+    head = backend.upload_quantized(hblob, Q6K, (VOCAB, D))
+    yield layers, blobs, head, hblob
+    for lw in layers:
+        for w in lw.values():
+            backend.release(w)
+    backend.release(head)
+
+
+def make_io(backend, B):
+    h0 = S.activations_f32(71 + B, B * D).reshape(B, D)
+    xo = S.activations_f32(72 + B, B * QR).reshape(B, QR)
+    xd = S.activations_f32(73 + B, B * FFN).reshape(B, FFN)
+    L = len(TYPES)
+    bufs = dict(
+        h=backend.upload(h0, shape=(B, D)),
+        h0=backend.upload(h0, shape=(B, D)),
+        x_o=backend.upload(xo, shape=(B, QR)),
+        x_down=backend.upload(xd, shape=(B, FFN)),
+        qkv=backend.upload(np.zeros(L * B * (QR + 2 * KVR), np.float32)),
+        gate_up=backend.upload(np.zeros(L * B * 2 * FFN, np.float32)),
+        logits=backend.upload(np.zeros(B * VOCAB, np.float32)),
+    )
+    return h0, xo, xd, bufs
+
+
+def read(backend, bufs, B):
+    L = len(TYPES)
+    return (
+        backend.download(bufs["h"]).reshape(B, D),
+        backend.download(bufs["qkv"]).reshape(L, B, QR + 2 * KVR),
+        backend.download(bufs["gate_up"]).reshape(L, B, 2 * FFN),
+        backend.download(bufs["logits"]).reshape(B, VOCAB),
+    )
+
+
+def eager(backend, layers, head, h0, xo, xd):
+    """The same step as single engine calls, one after another."""
+    B = h0.shape[0]
+
+    def up(a):
+        return backend.upload(a, shape=a.shape) if B > 1 else backend.upload(a[0])
+
+    def mv(w, x, add=None):
+        xb = up(x)
+        if add is None:
+            y = backend.quant_matvec(w, xb)
+        else:
+            ab = up(add)
+            y = backend.quant_matvec_add(w, xb, ab)
+            backend.release(ab)
+        out = backend.download(y).reshape(B, -1)
+        backend.release(y)
+        backend.release(xb)
+        return out
+
+    h = h0.copy()
+    qkvs, gus = [], []
+    for lw in layers:
+        qkvs.append(np.concatenate([mv(lw[n], h) for n in ("q", "k", "v")], axis=1))
+        h = mv(lw["o"], xo, h)
+        gus.append(np.concatenate([mv(lw[n], h) for n in ("gate", "up")], axis=1))
+        h = mv(lw["down"], xd, h)
+    return h, np.stack(qkvs), np.stack(gus), mv(head, h)
+
+
+def oracle_chain(blobs, hblob, h0, xo, xd):
+    def mm(qb, x):
+        qt, blob = qb
+        rows, cols = blob_shape[id(blob)]
+        return oracle.matmul_f64(qt.id, blob, rows, cols, x.astype(np.float32))
+
+    blob_shape = {}
+    for lb in blobs:
+        for name, (qt, blob) in lb.items():
+            blob_shape[id(blob)] = SHAPES[name]
+    blob_shape[id(hblob)] = (VOCAB, D)
+    h = h0.astype(np.float64)
+    qkvs, gus = [], []
+    for lb in blobs:
+        # the oracle takes fp32 activations; the residual is carried in fp64 between GEMVs
+        qkvs.append(np.concatenate([mm(lb[n], h) for n in ("q", "k", "v")], axis=1))
+        h = mm(lb["o"], xo) + h
+        gus.append(np.concatenate([mm(lb[n], h) for n in ("gate", "up")], axis=1))
+        h = mm(lb["down"], xd) + h
+    return h, np.stack(qkvs), np.stack(gus), mm((Q6K, hblob), h)
+
+
+@pytest.mark.parametrize("B", [1, 3, 16])
+def test_decode_plan_matches_eager_and_oracle(backend, model, B):
+    note("decode plan", "B", B)
+    layers, blobs, head, hblob = model
+    h0, xo, xd, bufs = make_io(backend, B)
+    io = {k: ptr(backend, bufs[k]) for k in ("h", "x_o", "x_down", "qkv", "gate_up", "logits")}
+    plan = backend.decode_plan(layers, head, B, io)
+    info = plan.info()
+    assert info["graph"] == 1 and info["layers"] == 2 and info["batch"] == B
+    assert (info["d_model"], info["qkv_rows"], info["ffn"], info["vocab"]) == (D, QR + 2 * KVR, FFN, VOCAB)
+    # layer 0: q|k|v, o, gate|up, down = 4 GEMVs; layer 1: q|k, v, o, gate, up, down = 6; head 1
+    assert info["gemvs_per_step"] == 11
+    total = sum(t.byte_size_for(SHAPES[n][0] * SHAPES[n][1]) for types in TYPES for n, t in types.items())
+    assert info["weight_bytes"] == total + Q6K.byte_size_for(VOCAB * D)
+
+    ref_eager = eager(backend, layers, head, h0, xo, xd)
+    ref64 = oracle_chain(blobs, hblob, h0, xo, xd)
+    lib = N.load()
+    first = None
+    for replay in range(3):
+        # reset the residual stream from its saved copy (a kernel, like the plan's own work)
+        assert lib.j4q_copy(C.c_void_p(io["h"]), C.c_void_p(ptr(backend, bufs["h0"])), B * D * 4, None) == 0
+        plan.run()
+        backend.sync()
+        got = read(backend, bufs, B)
+        for name, g, e, r in zip(("h", "qkv", "gate_up", "logits"), got, ref_eager, ref64):
+            assert np.array_equal(bits(g), bits(e)), f"replay {replay}: {name} differs from the eager calls"
+            assert rel_err(g.reshape(-1), r.reshape(-1)) <= 1e-4, f"replay {replay}: {name} vs oracle"
+        if first is None:
+            first = got
+        else:
+            for g, f in zip(got, first):
+                assert np.array_equal(bits(g), bits(f)), f"replay {replay} differs from the first"
+        # eager engine work between replays
+        x = backend.upload(S.activations_f32(replay, D))
+        y = backend.quant_matvec(layers[0]["q"], x)
+        backend.download(y)
+        backend.release(y)
+        backend.release(x)
+    plan.destroy()
+    for b in bufs.values():
+        backend.release(b)
+
+
+def test_decode_plan_errors(backend, model):
+    layers, _, head, _ = model
+    B = 1
+    _, _, _, bufs = make_io(backend, B)
+    io = {k: ptr(backend, bufs[k]) for k in ("h", "x_o", "x_down", "qkv", "gate_up", "logits")}
+    bad = [dict(layers[0]), dict(layers[1])]
+    bad[1]["o"] = layers[1]["down"]  # [512, 1024]: o must have d_model rows and o_cols columns
+    with pytest.raises(IllegalArgumentException, match="layer 1"):
+        backend.decode_plan(bad, head, B, io)
+    with pytest.raises(IllegalArgumentException, match="NULL"):
+        backend.decode_plan(layers, head, B, {**io, "x_o": 0})
+    with pytest.raises(IllegalArgumentException, match="aligned"):
+        backend.decode_plan(layers, head, B, {**io, "h": io["h"] + 4})
+    plan = backend.decode_plan(layers, None, B, io)
+    assert plan.info()["vocab"] == 0 and plan.info()["gemvs_per_step"] == 10
+    stale = DecodePlan(backend, plan.handle)
+    plan.destroy()
+    with pytest.raises(IllegalArgumentException, match="unknown or destroyed"):
+        stale.run()
+    for b in bufs.values():
+        backend.release(b)
