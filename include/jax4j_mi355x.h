@@ -178,6 +178,18 @@ int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *a
 int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, int8_t *xq_dev,
                           float *xs_dev, float *y_dev, void *stream);
 
+/* The prefill GEMM for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Same result as j4q_quant_matmul_into (bit for bit), but the int8 variant's
+ * workspace (the quantized activations and their block scales) lives in one fixed engine
+ * array of 36 MiB per GPU, so the call allocates nothing: x_dev bf16 [m, cols], y_dev fp32
+ * [m, rows], both 16-byte aligned. The int8 variant needs m * cols <= 33554432 (32 MiB of
+ * int8 activations, e.g. m = 8192 at cols = 4096), else J4Q_EUNSUPPORTED; the bf16 variant
+ * has no workspace. Every call on a GPU shares that GPU's workspace: calls that overlap on
+ * one GPU (on different streams, or from threads that do not order them) race. */
+int j4q_quant_matmul_noalloc(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, float *y_dev,
+                             void *stream);
+
 /* ---- decode-step plan (engine-local: QuantizedOps.quantMatvec / quantMatvecAdd,
  *      spi/QuantizedOps.java:27-30, composed over the layers of a decoder step) ---------- */
 /* The quantized matmuls of an n-layer decode step, built once and replayed as one captured

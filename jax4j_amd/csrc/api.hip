@@ -32,8 +32,20 @@ struct Buf {
     bool live = false;
 };
 
+// Workspace of j4q_quant_matmul_noalloc (the one entry point that allocates nothing): the
+// int8 activations [m, K] of one call in the first 32 MiB, their fp32 block scales
+// [m, K / 32] (at most 4 MiB for m * K <= 32 MiB) after them. Every GPU the library runs on
+// holds its own copy until the process ends; host code never passes `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address) but the address
+// hipGetSymbolAddress returns for the engine's device, kept in g_scratch. Calls that overlap
+// on one GPU share it and race.
+constexpr uint64_t kScratchQBytes = 32ull << 20;
+constexpr uint64_t kScratchBytes = kScratchQBytes + (4ull << 20);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 std::mutex g_mu;
 std::vector<Buf> g_bufs;
+void *g_scratch = nullptr;  // device address of `scratch` on g_dev
 std::vector<uint32_t> g_free;
 bool g_ready = false;
 int g_dev = -1;
@@ -106,6 +118,8 @@ int init_locked(int device) {
     HIP_TRY("hipGetDeviceProperties", hipGetDeviceProperties(&p, device));
     if (!is_gfx950(p)) return fail(J4Q_ENODEV, "device %d is %s; this engine is built for gfx950 only", device, p.gcnArchName);
     HIP_TRY("hipSetDevice", hipSetDevice(device));
+    // the engine serves one device per process, so one address of the workspace is kept
+    HIP_TRY("hipGetSymbolAddress", hipGetSymbolAddress(&g_scratch, HIP_SYMBOL(scratch)));
     HIP_TRY("hipStreamCreateWithFlags", hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     j4q::gemv_set_cus(p.multiProcessorCount);
     g_dev = device;
@@ -783,6 +797,37 @@ int j4q_quant_matmul_into(j4q_buffer wh, const uint16_t *x, int64_t m, int varia
     }
     HIP_TRY("quantMatmul_into", j4q::launch_quantize_act(x, m, mm.cols, xq, xs, s));
     HIP_TRY("quantMatmul_into", j4q::launch_gemm_q8_int8(mm, xq, xs, y, m, s));
+    return J4Q_OK;
+}
+
+int j4q_quant_matmul_noalloc(j4q_buffer wh, const uint16_t *x, int64_t m, int variant, float *y, void *stream) {
+    if (!x || !y) return fail(J4Q_EINVAL, "quantMatmul_noalloc: NULL x or y");
+    if (variant != J4Q_GEMM_INT8 && variant != J4Q_GEMM_BF16)
+        return fail(J4Q_EUNSUPPORTED, "quantMatmul_noalloc: unknown variant %d", variant);
+    if (!aligned(x, 16) || !aligned(y, 16)) return fail(J4Q_EINVAL, "quantMatmul_noalloc: pointers must be 16-byte aligned");
+    if (m <= 0) return fail(J4Q_EINVAL, "quantMatmul_noalloc: m must be positive");
+    std::lock_guard<std::mutex> lk(g_mu);
+    Buf *w;
+    int rc;
+    if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatmul_noalloc", &w))) return rc;
+    if (w->qtype != J4Q_Q8_0) return fail(J4Q_EUNSUPPORTED, "quantMatmul_noalloc: only Q8_0 weights are supported");
+    const int64_t K = w->dims[1];
+    if ((rc = check_gemm_size(m, K, variant, "quantMatmul_noalloc"))) return rc;
+    if (variant == J4Q_GEMM_INT8 && (uint64_t)m * (uint64_t)K > kScratchQBytes)
+        return fail(J4Q_EUNSUPPORTED,
+                    "quantMatmul_noalloc: the int8 variant's workspace holds m * cols <= %llu values, got %lld x %lld",
+                    (unsigned long long)kScratchQBytes, (long long)m, (long long)K);
+    if ((rc = ensure_ready())) return rc;
+    const hipStream_t s = pick_stream(stream);
+    const j4q::QMat mm = qmat_of(*w);
+    if (variant == J4Q_GEMM_BF16) {
+        HIP_TRY("quantMatmul_noalloc", j4q::launch_gemm_q8_bf16(mm, x, y, m, s));
+        return J4Q_OK;
+    }
+    int8_t *xq = (int8_t *)g_scratch;
+    float *xs = (float *)((uint8_t *)g_scratch + kScratchQBytes);
+    HIP_TRY("quantMatmul_noalloc", j4q::launch_quantize_act(x, m, K, xq, xs, s));
+    HIP_TRY("quantMatmul_noalloc", j4q::launch_gemm_q8_int8(mm, xq, xs, y, m, s));
     return J4Q_OK;
 }
 
