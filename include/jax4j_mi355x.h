@@ -164,12 +164,15 @@ int j4q_quantize_act(j4q_buffer x_bf16, j4q_buffer *xq_i8, j4q_buffer *scales_f3
  * MFMA on W dequantized into LDS. */
 int j4q_quant_matmul(j4q_buffer weights, j4q_buffer x, int variant, j4q_buffer *y);
 
-/* ---- stream-ordered entry points on caller memory (no allocation, no sync) ------------- */
+/* ---- stream-ordered entry points on caller memory (no sync) ----------------------------- */
 
 /* quantMatvec / quantMatvecAdd into caller device memory: x_dev [batch, cols] and y_dev
  * [batch, rows] fp32 (16-byte aligned); add_dev NULL or [batch, rows]. add_dev may be y_dev
- * itself (a residual updated in place) for cols <= 32768; above that an add overlapping y
- * returns J4Q_EUNSUPPORTED (the column windows would read it after rewriting y). */
+ * itself (a residual updated in place) for cols <= 32768, or at batch >= 3 on Q4_0, Q8_0,
+ * Q4_K and Q6_K; other adds overlapping y return J4Q_EUNSUPPORTED (column windows chained
+ * one after another would read it after rewriting y). A batched call over several column
+ * windows keeps their partial sums in stream-ordered memory of `stream` (hipMallocAsync /
+ * hipFreeAsync, batch x rows x windows floats); nothing else is allocated. */
 int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *add_dev, float *y_dev,
                           int64_t batch, void *stream);
 /* Prefill GEMM into caller memory. x_dev bf16 [m, cols]; y_dev fp32 [m, rows]. The int8

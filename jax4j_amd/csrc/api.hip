@@ -336,7 +336,22 @@ int matvec_common(j4q_buffer wh, j4q_buffer xh, j4q_buffer addh, j4q_buffer *out
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, B == 1 ? 1 : 2, B == 1 ? N : B, B == 1 ? 0 : N, (uint64_t)(B * N) * 4, out, &ydev)))
         return rc;
-    LAUNCH_INTO(op, out, j4q::launch_gemv(qt, m, (const float *)xdev, (const float *)adev, (float *)ydev, B, g_stream));
+    // a batched call over several column windows runs them in one launch on a stream-ordered
+    // workspace for their partial sums; if it cannot be had, the windows run one after another
+    j4q::Workspace ws;
+    const uint64_t wsb = j4q::gemv_workspace_bytes(qt, m, B);
+    if (wsb) {
+        void *p = nullptr;
+        if (hipMallocAsync(&p, wsb, g_stream) == hipSuccess) {
+            ws.ptr = (float *)p;
+            ws.bytes = wsb;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
+    const hipError_t e = j4q::launch_gemv(qt, m, (const float *)xdev, (const float *)adev, (float *)ydev, B, g_stream, ws);
+    if (ws.ptr) (void)hipFreeAsync(ws.ptr, g_stream);
+    LAUNCH_INTO(op, out, e);
     return J4Q_OK;
 }
 
@@ -765,12 +780,26 @@ int j4q_quant_matvec_into(j4q_buffer wh, const float *x, const float *add, float
     int rc;
     if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatvec_into", &w))) return rc;
     const int64_t N = w->dims[0], K = w->dims[1];
-    if (add && add < y + batch * N && y < add + batch * N && K > j4q::gemv_single_pass_cols())
+    const j4q::QMat m = qmat_of(*w);
+    if (add && add < y + batch * N && y < add + batch * N && !j4q::gemv_in_place_ok(w->qtype, m, batch))
         return fail(J4Q_EUNSUPPORTED,
-                    "quantMatvec_into: an add that overlaps y needs cols <= %lld (one column window), got %lld",
-                    (long long)j4q::gemv_single_pass_cols(), (long long)K);
+                    "quantMatvec_into: an add that overlaps y needs cols <= %lld (one column window) or batch >= 3 on "
+                    "Q4_0/Q8_0/Q4_K/Q6_K, got cols %lld, batch %lld",
+                    (long long)j4q::gemv_single_pass_cols(), (long long)K, (long long)batch);
     if ((rc = ensure_ready())) return rc;
-    HIP_TRY("quantMatvec_into", j4q::launch_gemv(w->qtype, qmat_of(*w), x, add, y, batch, pick_stream(stream)));
+    const hipStream_t s = pick_stream(stream);
+    // partial sums of several column windows live in stream-ordered memory of the call's stream
+    j4q::Workspace ws;
+    const uint64_t wsb = j4q::gemv_workspace_bytes(w->qtype, m, batch);
+    if (wsb) {
+        void *p = nullptr;
+        HIP_TRY("hipMallocAsync", hipMallocAsync(&p, wsb, s));
+        ws.ptr = (float *)p;
+        ws.bytes = wsb;
+    }
+    const hipError_t e = j4q::launch_gemv(w->qtype, m, x, add, y, batch, s, ws);
+    if (ws.ptr) (void)hipFreeAsync(ws.ptr, s);
+    HIP_TRY("quantMatvec_into", e);
     return J4Q_OK;
 }
 

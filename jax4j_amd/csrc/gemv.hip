@@ -45,56 +45,107 @@ hipError_t launch_fmt(const QMat &m, const float *x, const float *add, float *y,
 
 int g_cus = 256;
 
-// Items per wave of launch_mfma: 8 waves x items x blocks per item is the launch window,
-// 128 blocks (4096 columns) for up to 8 batch rows; 64 blocks at 16 rows, whose x image of
-// 16 rows x 4096 columns would not fit in LDS.
-// Waves per workgroup: 16 for Q8_0 and Q4_0 up to 8 rows (half the items per wave, twice the
-// waves to hide the load latency: Q8_0 4096 x 4096 at B = 8 12.8 -> 10.9 us, Q4_0 11008 x
-// 4096 12.4 -> 12.0 us; Q4_K was 2 % slower and Q6_K spilled registers), else 8. The window
-// (waves x items x blocks per item) is the same either way.
+// Waves per workgroup and items per wave of launch_mfma (waves x items x blocks per item is
+// the launch window):
+//  - up to 8 rows: windows of 128 blocks (4096 columns); 16 waves for Q8_0 and Q4_0 (half
+//    the items per wave, twice the waves to hide the load latency: Q8_0 4096 x 4096 at B = 8
+//    12.8 -> 10.9 us, Q4_0 11008 x 4096 12.4 -> 12.0 us; Q4_K was 2 % slower and Q6_K spilled
+//    registers), else 8;
+//  - 9..16 rows: 4 waves of 8 blocks, windows of 32 blocks (1024 columns, a 64 KB x image,
+//    two workgroups per CU). Measured on the B = 16 decode step (all windows of a matrix in
+//    one launch): 3.41 ms at 4 waves, 3.42 ms at 8 (2048-column windows); either way a CU
+//    holds 8 waves, the LDS the x images take.
 template <int FMT, int BB>
-constexpr int mfma_waves() { return BB <= 8 && (FMT == Q8_0 || FMT == Q4_0) ? 16 : 8; }
+constexpr int mfma_waves() { return BB > 8 ? 4 : (FMT == Q8_0 || FMT == Q4_0) ? 16 : 8; }
 template <int FMT, int BB>
-constexpr int mfma_ipw() { return (FMT == Q8_0 ? 8 : 4) / (BB > 8 ? 2 : 1) * 8 / mfma_waves<FMT, BB>(); }
+constexpr int mfma_ipw() { return BB > 8 ? (FMT == Q8_0 ? 4 : 2) : (FMT == Q8_0 ? 8 : 4) * 8 / mfma_waves<FMT, BB>(); }
 template <int FMT, int BB>
 constexpr int mfma_window() { return mfma_waves<FMT, BB>() * mfma_ipw<FMT, BB>() * (FMT == Q8_0 ? 2 : 4); }
 
-// Batched GEMV on the matrix cores (gemv_mfma.h) for up to 16 batch rows per launch:
-// persistent grid of one workgroup per CU, each launch a window of up to 128 blocks (4096
-// columns; 64 at 16 rows) split into one slice per wave; a wider K runs as equal windows,
-// each adding the previous window's output. Measured on MI355X (Q4_0 11008 x 4096): B = 4
-// 10.8 us, B = 8 12.4 us, against 22 us and 41 us for one vector-ALU pass per batch row;
-// at B <= 2 the two are level. The Llama-3-8B decode step at B = 16 takes 4.8 ms with one
-// 16-row pass per matrix, 6.1 ms with two 8-row passes.
+// Column windows of a matrix for a launch of BB batch rows: windows of at most CAP blocks,
+// equal, aligned to whole items (K-quants: to whole 8-block superblocks, so each wave's
+// slice starts a superblock).
 template <int FMT, int BB>
-hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
-    constexpr int W = mfma_waves<FMT, BB>(), IPW = mfma_ipw<FMT, BB>(), S = FMT == Q8_0 ? 2 : 4;
-    constexpr int CAP = mfma_window<FMT, BB>();
-    static_assert(CAP == W * IPW * S && CAP == (BB > 8 ? 64 : 128), "window = waves x items per wave x blocks per item");
-    const int tiles = (int)((m.rows + 15) / 16);
-    const int grid = tiles < g_cus ? tiles : g_cus;
-    const int nb = (int)(m.cols / 32);
-    const int windows = (nb + CAP - 1) / CAP;
-    // equal windows, aligned to whole items (K-quants: to whole 8-block superblocks, so each
-    // wave's slice starts a superblock)
+void mfma_windows(const QMat &m, int &windows, int &per) {
+    constexpr int S = FMT == Q8_0 ? 2 : 4, CAP = mfma_window<FMT, BB>();
     constexpr int AL = FMT == Q4_K || FMT == Q6_K ? 8 : S;
     static_assert(CAP % AL == 0, "windows fit the cap");
-    const int per = ((nb + windows - 1) / windows + AL - 1) / AL * AL;
+    const int nb = (int)(m.cols / 32);
+    windows = (nb + CAP - 1) / CAP;
+    per = ((nb + windows - 1) / windows + AL - 1) / AL * AL;
+    windows = (nb + per - 1) / per;
+}
+
+// Batched GEMV on the matrix cores (gemv_mfma.h) for up to 16 batch rows per launch,
+// persistent workgroups of 16-row tiles, each launch window of up to 128 blocks (4096
+// columns; 64 at 16 rows) split into one slice per wave. A wider K has several windows:
+// with a workspace they all run in one launch (grid.y = window, about CUs / windows
+// workgroups each, every CU holding one window's x image) and sum_windows_kernel adds
+// their sums in window order; without one they run as launches chained through prev (the
+// same additions in the same order). Measured on MI355X (Q4_0 11008 x 4096): B = 4 10.8 us,
+// B = 8 12.4 us, against 22 us and 41 us for one vector-ALU pass per batch row; at B <= 2
+// the two are level.
+template <int FMT, int BB>
+hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y, int b, const Workspace &ws,
+                       hipStream_t s) {
+    constexpr int W = mfma_waves<FMT, BB>(), IPW = mfma_ipw<FMT, BB>(), S = FMT == Q8_0 ? 2 : 4;
+    constexpr int CAP = mfma_window<FMT, BB>();
+    static_assert(CAP == W * IPW * S && CAP == (BB > 8 ? 8 * W : 128), "window = waves x items per wave x blocks per item");
+    const int tiles = (int)((m.rows + 15) / 16);
+    const int nb = (int)(m.cols / 32);
+    int windows, per;
+    mfma_windows<FMT, BB>(m, windows, per);
+    const uint64_t need = windows > 1 ? (uint64_t)windows * (uint64_t)b * (uint64_t)m.rows * 4u : 0;
+    if (windows == 1 || (ws.ptr && ws.bytes >= need)) {
+        // workgroups resident at once (LDS-bound), shared out between the windows
+        constexpr int lds = gmf::Plan<BB, gmf::Fmt<FMT>::GROUPS, W, IPW * S, gmf::round_tiles<BB, W>()>::kBytes;
+        constexpr int per_cu = 163840 / lds > 0 ? 163840 / lds : 1;
+        int grid = (g_cus * (per_cu < 8 ? per_cu : 8) + windows - 1) / windows;
+        if (grid > tiles) grid = tiles;
+        hipError_t e = gmf::launch_k<FMT, BB, W, IPW, false, 2>(m, x, windows == 1 ? add : nullptr, y, b, grid, s, 0, per,
+                                                                nb, nullptr, windows, ws.ptr);
+        if (e != hipSuccess || windows == 1) return e;
+        const int64_t n = (int64_t)b * m.rows;
+        const int64_t blocks = (n + 255) / 256;
+        gmf::sum_windows_kernel<<<(unsigned)(blocks < 2048 ? blocks : 2048), 256, 0, s>>>(ws.ptr, windows, n, add, y);
+        return hipGetLastError();
+    }
+    const int grid = tiles < g_cus ? tiles : g_cus;
     for (int kb0 = 0; kb0 < nb; kb0 += per) {
-        const int kbn = nb - kb0 < per ? nb - kb0 : per;
-        const bool last = kb0 + kbn >= nb;
-        const hipError_t e = gmf::launch_k<FMT, BB, W, IPW, false, 2>(m, x, last ? add : nullptr, y, b, grid, s, kb0, kbn,
-                                                                        kb0 == 0 ? nullptr : y);
+        const bool last = kb0 + per >= nb;
+        const hipError_t e = gmf::launch_k<FMT, BB, W, IPW, false, 2>(m, x, last ? add : nullptr, y, b, grid, s, kb0, per,
+                                                                        last ? nb : kb0 + per, kb0 == 0 ? nullptr : y, 1,
+                                                                        nullptr);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }
 
 template <int FMT>
-hipError_t launch_mfma_fmt(const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
-    if (b <= 4) return launch_mfma<FMT, 4>(m, x, add, y, b, s);
-    if (b <= 8) return launch_mfma<FMT, 8>(m, x, add, y, b, s);
-    return launch_mfma<FMT, 16>(m, x, add, y, b, s);
+hipError_t launch_mfma_fmt(const QMat &m, const float *x, const float *add, float *y, int b, const Workspace &ws,
+                           hipStream_t s) {
+    if (b <= 4) return launch_mfma<FMT, 4>(m, x, add, y, b, ws, s);
+    if (b <= 8) return launch_mfma<FMT, 8>(m, x, add, y, b, ws, s);
+    return launch_mfma<FMT, 16>(m, x, add, y, b, ws, s);
+}
+
+template <int FMT>
+uint64_t mfma_ws_fmt(const QMat &m, int b) {
+    int windows = 1, per = 0;
+    if (b <= 4) mfma_windows<FMT, 4>(m, windows, per);
+    else if (b <= 8) mfma_windows<FMT, 8>(m, windows, per);
+    else mfma_windows<FMT, 16>(m, windows, per);
+    return windows > 1 ? (uint64_t)windows * (uint64_t)b * (uint64_t)m.rows * 4u : 0;
+}
+
+uint64_t mfma_ws_any(int id, const QMat &m, int b) {
+    switch (id) {
+    case Q4_0: return mfma_ws_fmt<Q4_0>(m, b);
+    case Q4_K: return mfma_ws_fmt<Q4_K>(m, b);
+    case Q6_K: return mfma_ws_fmt<Q6_K>(m, b);
+    case Q8_0: return mfma_ws_fmt<Q8_0>(m, b);
+    default: return 0;
+    }
 }
 
 // Several windows read add only in the last one, after y was rewritten: an add that
@@ -102,9 +153,8 @@ hipError_t launch_mfma_fmt(const QMat &m, const float *x, const float *add, floa
 template <int BB>
 bool single_window(const QMat &m) { return m.cols <= 32 * mfma_window<Q4_0, BB>(); }
 
-bool mfma_supported(int id, const QMat &m, bool add_aliases_y) {
+bool mfma_format(int id, const QMat &m) {
     const int64_t k = m.cols;
-    if (add_aliases_y && !single_window<8>(m)) return false;
     switch (id) {
     case Q4_0: case Q4_K: case Q6_K: return k % 128 == 0;
     case Q8_0: return k % 64 == 0;
@@ -112,12 +162,13 @@ bool mfma_supported(int id, const QMat &m, bool add_aliases_y) {
     }
 }
 
-hipError_t launch_mfma_any(int id, const QMat &m, const float *x, const float *add, float *y, int b, hipStream_t s) {
+hipError_t launch_mfma_any(int id, const QMat &m, const float *x, const float *add, float *y, int b, const Workspace &ws,
+                           hipStream_t s) {
     switch (id) {
-    case Q4_0: return launch_mfma_fmt<Q4_0>(m, x, add, y, b, s);
-    case Q4_K: return launch_mfma_fmt<Q4_K>(m, x, add, y, b, s);
-    case Q6_K: return launch_mfma_fmt<Q6_K>(m, x, add, y, b, s);
-    case Q8_0: return launch_mfma_fmt<Q8_0>(m, x, add, y, b, s);
+    case Q4_0: return launch_mfma_fmt<Q4_0>(m, x, add, y, b, ws, s);
+    case Q4_K: return launch_mfma_fmt<Q4_K>(m, x, add, y, b, ws, s);
+    case Q6_K: return launch_mfma_fmt<Q6_K>(m, x, add, y, b, ws, s);
+    case Q8_0: return launch_mfma_fmt<Q8_0>(m, x, add, y, b, ws, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -137,23 +188,45 @@ hipError_t launch_valu(int id, const QMat &m, const float *x, const float *add, 
 
 void gemv_set_cus(int cus) { g_cus = cus > 0 ? cus : 256; }
 
+bool gemv_in_place_ok(int id, const QMat &m, int64_t batch) {
+    return m.cols <= gemv::kMaxWindow || (batch >= 3 && mfma_format(id, m));
+}
+
+uint64_t gemv_workspace_bytes(int id, const QMat &m, int64_t batch) {
+    if (batch < 3 || m.rows <= 0 || !mfma_format(id, m)) return 0;
+    // launches of 16 rows and, for a remainder of 3..15 rows, one smaller launch
+    uint64_t need = mfma_ws_any(id, m, (int)(batch < 16 ? batch : 16));
+    const int64_t rem = batch % 16;
+    if (batch > 16 && rem >= 3) {
+        const uint64_t r = mfma_ws_any(id, m, (int)rem);
+        if (r > need) need = r;
+    }
+    return need;
+}
+
 hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, float *y, int64_t batch,
-                       hipStream_t s) {
+                       hipStream_t s, const Workspace &ws) {
     if (m.rows <= 0 || batch <= 0) return hipSuccess;
     if (batch > 65535 || m.rows > (1 << 30) || m.cols > 0x7fffffff) return hipErrorInvalidValue;
     const bool alias = add && add < y + batch * m.rows && y < add + batch * m.rows;
-    if (alias && m.cols > gemv::kMaxWindow) return hipErrorInvalidValue;
-    if (batch < 3 || !mfma_supported(id, m, alias)) return launch_valu(id, m, x, add, y, (int)batch, s);
-    // batch rows in launches of up to 16 on the matrix cores (9..16 rows stream W once, in
-    // windows of 2048 columns); a remainder of 1 or 2 rows takes the vector-ALU kernel,
-    // which is as fast there
-    const int64_t cap = !alias || single_window<16>(m) ? 16 : 8;
+    const bool mfma = batch >= 3 && mfma_format(id, m);
+    // with the workspace, several windows meet in sum_windows_kernel, which reads each add
+    // element before it writes y there; without it they are chained launches that would
+    // read an add overlapping y after rewriting y, so such a call keeps one window
+    const bool ws_ok = mfma && ws.ptr && ws.bytes >= gemv_workspace_bytes(id, m, batch);
+    if (!mfma || (alias && !ws_ok && !single_window<8>(m))) {
+        if (alias && m.cols > gemv::kMaxWindow) return hipErrorInvalidValue;
+        return launch_valu(id, m, x, add, y, (int)batch, s);
+    }
+    // batch rows in launches of up to 16 on the matrix cores (every launch streams W once for
+    // its rows); a remainder of 1 or 2 rows takes the vector-ALU kernel, which is as fast there
+    const int64_t cap = !alias || ws_ok || single_window<16>(m) ? 16 : 8;
     for (int64_t b0 = 0; b0 < batch;) {
         const int64_t nb = batch - b0 < cap ? batch - b0 : cap;
         const float *xb = x + b0 * m.cols;
         const float *ab = add ? add + b0 * m.rows : nullptr;
         float *yb = y + b0 * m.rows;
-        const hipError_t e = nb >= 3 ? launch_mfma_any(id, m, xb, ab, yb, (int)nb, s)
+        const hipError_t e = nb >= 3 ? launch_mfma_any(id, m, xb, ab, yb, (int)nb, ws_ok ? ws : Workspace(), s)
                                      : launch_valu(id, m, xb, ab, yb, (int)nb, s);
         if (e != hipSuccess) return e;
         b0 += nb;

@@ -174,11 +174,13 @@ struct Plan {
 template <int BB, int WAVES>
 constexpr int round_tiles() { return BB <= 8 && WAVES <= 8 ? 4 : 2; }
 
-// grid: G_wg persistent workgroups of WAVES waves; workgroup w takes 16-row tiles w,
-// w + G_wg, ... The kernel covers the window of blocks [kb0, kb0 + kbn) of every row:
-// y = (W[:, window] x[window] + prev) + add, so a wider K runs as windows chained through
-// prev (each adding the previous window's y, read before that element is rewritten) and
-// the caller's add joins only in the last window.
+// grid: (G_wg, R) persistent workgroups of WAVES waves; workgroup (w, r) takes 16-row tiles
+// w, w + G_wg, ... of window r, the blocks [kb0 + r per, min(kb0 + (r + 1) per, nbe)) of
+// every row. With part == nullptr (R = 1) the launch writes y = (W[:, window] x[window] +
+// prev) + add, so windows can also run one launch after another, chained through prev
+// (each adding the previous window's y, read before that element is rewritten) with the
+// caller's add joining only in the last. With wsum, every window writes its own sums to
+// wsum[r][b][row] (no prev, no add) and sum_windows_kernel adds them in window order.
 // Wave v owns window blocks [v NBW, (v + 1) NBW) (NBW = IPW * S); blocks past the window
 // load nothing and their x image is zero. Requires kb0 and kbn multiples of S (Q4_K, Q6_K:
 // of 8, so every slice starts on a superblock), kbn <= WAVES * NBW and B <= BB. XREG keeps
@@ -187,7 +189,14 @@ constexpr int round_tiles() { return BB <= 8 && WAVES <= 8 ? 4 : 2; }
 template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS>
 __global__ void __launch_bounds__(WAVES * 64)
 gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const float *__restrict__ add, float *y,
-                 int B, int kb0, int kbn) {
+                 int B, int kb0, int per, int nbe, float *__restrict__ wsum) {
+    kb0 += (int)blockIdx.y * per;
+    const int kbn = nbe - kb0 < per ? nbe - kb0 : per;
+    if (wsum) {
+        wsum += (int64_t)blockIdx.y * B * m.rows;
+        prev = nullptr;
+        add = nullptr;
+    }
     using F = Fmt<FMT>;
     constexpr int S = F::S, G = F::GROUPS, NBW = IPW * S;
     constexpr bool W16 = BB == 16;  // two A operands (hi, lo) of 16 batch rows each
@@ -195,6 +204,8 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     constexpr int RT = round_tiles<BB, WAVES>();
     static_assert(RT % TS == 0, "a round holds whole turns of the tile ring");
     using P = Plan<BB, G, WAVES, NBW, RT>;
+    // threads (b, nn) < 16 BB fetch a tile's prev / add values with its weights
+    static_assert(WAVES * 64 >= BB * 16, "one thread per output of a tile");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int K = (int)m.cols, N = (int)m.rows;
     const int tiles = (N + 15) / 16, nb = kb0 + kbn;  // blocks [kb0, nb) of every row
@@ -596,10 +607,12 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     // End of a round of ns tiles starting at tile t: thread (k, b, nn) adds the waves'
     // partials of output (b, row 16 (t + k tstep) + nn) in wave order. The second barrier
     // keeps the slots until every reader is done.
+    // The round's ns x BB x 16 outputs are dealt to the threads (more outputs than threads
+    // when the workgroup is small: 4 waves at BB = 16 take one tile per pass).
     auto finish = [&](int t, int ns) {
         __syncthreads();
-        const int k = (int)threadIdx.x / (BB * 16), o = (int)threadIdx.x % (BB * 16);
-        if (k < ns) {
+        for (int i = (int)threadIdx.x; i < ns * BB * 16; i += WAVES * 64) {
+            const int k = i / (BB * 16), o = i % (BB * 16);
             const int b = o >> 4, nn = o & 15;
             const float *pp = part + k * (WAVES * BB * 16);
             float s = 0.f;
@@ -608,7 +621,10 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             const int r = (t + k * tstep) * 16 + nn;
             // the previous window's sum first, then add on its own: fl(fl(W.x) + add)
             if (prev) s += av.x;
-            if (b < B && r < N) y[(int64_t)b * N + r] = add ? s + av.y : s;
+            if (b < B && r < N) {
+                if (wsum) wsum[(int64_t)b * N + r] = s;
+                else y[(int64_t)b * N + r] = add ? s + av.y : s;
+            }
         }
         __syncthreads();
     };
@@ -631,15 +647,31 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     }
 }
 
+// One launch: `windows` windows of `per` blocks from kb0 (the last ends at nbe), `grid`
+// workgroups each; several windows need `part` (windows x B x rows floats).
 template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS = 2>
-hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, int B, int grid, hipStream_t s,
-                    int kb0 = 0, int kbn = -1, const float *prev = nullptr) {
-    if (kbn < 0) kbn = (int)(m.cols / 32);
+hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, int B, int grid, hipStream_t s, int kb0,
+                    int per, int nbe, const float *prev, int windows, float *part) {
     constexpr int NBW = IPW * Fmt<FMT>::S;
     constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW, round_tiles<BB, WAVES>()>::kBytes;
     static_assert(lds <= 160 * 1024, "LDS of one workgroup");
-    gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<grid, WAVES * 64, lds, s>>>(m, x, prev, add, y, B, kb0, kbn);
+    if (windows > 1 && !part) return hipErrorInvalidValue;
+    gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<dim3(grid, windows), WAVES * 64, lds, s>>>(
+        m, x, prev, add, y, B, kb0, per, nbe, windows > 1 ? part : nullptr);
     return hipGetLastError();
+}
+
+// y[i] = ((part[0][i] + part[1][i]) + ...) + add[i] for i < n (= B x rows): the windows'
+// sums in window order (the same additions as windows chained through prev), then the add
+// on its own. Each element is read and written by one thread, so add may be y itself.
+__global__ void __launch_bounds__(256)
+sum_windows_kernel(const float *__restrict__ part, int windows, int64_t n, const float *add, float *y) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        float v = part[i];
+        for (int r = 1; r < windows; r++) v += part[(int64_t)r * n + i];
+        if (add) v += add[i];
+        y[i] = v;
+    }
 }
 
 }  // namespace gmf

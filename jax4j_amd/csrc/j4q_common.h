@@ -124,8 +124,20 @@ hipError_t launch_export(int id, const uint8_t *split, uint8_t *gguf, int64_t ro
                          hipStream_t s);
 hipError_t launch_dequant_rows(int id, const QMat &m, int64_t row0, int64_t nrows, float *out,
                                hipStream_t s);
+// Device scratch a batched GEMV may use for the partial sums of its column windows.
+struct Workspace {
+    float *ptr = nullptr;
+    uint64_t bytes = 0;
+};
+// Bytes of workspace a batched GEMV of `batch` rows uses to run all its column windows in one
+// launch (0 when it has one window, or does not run on the matrix cores). With less, the
+// windows run one launch after another.
+uint64_t gemv_workspace_bytes(int id, const QMat &m, int64_t batch);
+// Whether an add that overlaps y is served for this matrix and batch (given the workspace
+// gemv_workspace_bytes asks for): one column window, or the matrix-core path.
+bool gemv_in_place_ok(int id, const QMat &m, int64_t batch);
 hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, float *y, int64_t batch,
-                       hipStream_t s);
+                       hipStream_t s, const Workspace &ws = Workspace());
 hipError_t launch_quantize_act(const uint16_t *x, int64_t m, int64_t k, int8_t *q, float *scales,
                                hipStream_t s);
 hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs, float *y, int64_t m,

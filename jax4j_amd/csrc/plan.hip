@@ -55,6 +55,7 @@ struct Op {
 struct Plan {
     j4q_decode_plan_desc desc{};
     int64_t batch = 0;
+    Workspace ws;  // partial sums of batched GEMVs over several column windows (plan-owned)
     std::vector<Op> ops;
     std::vector<void *> owned;
     hipGraph_t graph = nullptr;
@@ -69,7 +70,7 @@ hipError_t enqueue(const Plan &p, hipStream_t s) {
     for (const Op &o : p.ops) {
         hipError_t e;
         if (o.gemv) {
-            e = launch_gemv(o.qt, o.m, o.x, o.add, o.y, p.batch, s);
+            e = launch_gemv(o.qt, o.m, o.x, o.add, o.y, p.batch, s, p.ws);
         } else {
             const int64_t n = o.cols * p.batch;
             const int64_t blocks = (n + 255) / 256;
@@ -261,6 +262,23 @@ int j4q_decode_plan_create(const j4q_decode_layer *layers, int32_t n_layers, j4q
         if (!rc) rc = one_gemv(p, L.down, "decode plan down", io->x_down, h_alt, h);
     }
     if (!rc && head) rc = one_gemv(p, head, "decode plan head", h, nullptr, io->logits);
+    uint64_t wsb = 0;
+    for (const Op &o : p.ops) {
+        const uint64_t b = o.gemv ? gemv_workspace_bytes(o.qt, o.m, batch) : 0;
+        if (b > wsb) wsb = b;
+    }
+    if (!rc && wsb) {
+        void *d = nullptr;
+        e = hipMalloc(&d, wsb);
+        if (e != hipSuccess) {
+            rc = report_hip("decode plan workspace", e);
+        } else {
+            p.owned.push_back(d);
+            p.ws.ptr = (float *)d;
+            p.ws.bytes = wsb;
+            p.desc.plan_bytes += wsb;
+        }
+    }
     if (rc) {
         free_plan(p);
         return rc;
