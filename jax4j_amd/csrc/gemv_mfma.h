@@ -202,7 +202,10 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     constexpr bool W16 = BB == 16;  // two A operands (hi, lo) of 16 batch rows each
     static_assert(BB <= 8 || (W16 && !XREG), "BB up to 8, or 16 without XREG");
     constexpr int RT = round_tiles<BB, WAVES>();
-    static_assert(RT % TS == 0, "a round holds whole turns of the tile ring");
+    // the tile ring (TS tiles in flight) and the rounds (RT tiles per reduction) advance
+    // together through super-rounds of SR tiles, so every ring slot index is a constant
+    constexpr int SR = RT > TS ? RT : TS;
+    static_assert(SR % RT == 0 && SR % TS == 0, "rounds and ring turns tile a super-round");
     using P = Plan<BB, G, WAVES, NBW, RT>;
     // threads (b, nn) < 16 BB fetch a tile's prev / add values with its weights
     static_assert(WAVES * 64 >= BB * 16, "one thread per output of a tile");
@@ -633,17 +636,23 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     // computed. Waves run through a round of RT tiles without waiting for each other; the
     // partial sums meet at the round's end. The tile loop is workgroup-uniform, so every
     // wave reaches each barrier.
-    for (int t = t0; t < tiles; t += RT * tstep) {
-        int ns = 0;
+    for (int t = t0; t < tiles; t += SR * tstep) {
 #pragma unroll
-        for (int k = 0; k < RT; k++) {
-            const int tk = t + k * tstep;
-            if (tk >= tiles) break;
-            process(tset[k % TS], avs[k % TS], k);
-            load_tile(tset[k % TS], avs[k % TS], tk + TS * tstep);
-            ns = k + 1;
+        for (int rr = 0; rr < SR / RT; rr++) {
+            const int tr = t + rr * RT * tstep;
+            if (tr >= tiles) break;
+            int ns = 0;
+#pragma unroll
+            for (int k = 0; k < RT; k++) {
+                const int tk = tr + k * tstep;
+                if (tk >= tiles) break;
+                const int slot = (rr * RT + k) % TS;
+                process(tset[slot], avs[slot], k);
+                load_tile(tset[slot], avs[slot], tk + TS * tstep);
+                ns = k + 1;
+            }
+            finish(tr, ns);
         }
-        finish(t, ns);
     }
 }
 
