@@ -252,7 +252,8 @@ class Mi355xBackend:
         return s.value or 0
 
     def quant_matvec_into(self, weights: DeviceBuffer, x_ptr: int, add_ptr: int, y_ptr: int, batch: int = 1, stream: int = 0) -> None:
-        """Stream-ordered GEMV on caller device memory; allocates nothing, does not sync."""
+        """Stream-ordered GEMV on caller device memory; does not sync. A batched call over
+        several column windows takes its partial-sum workspace from stream-ordered memory."""
         check(
             self._lib().j4q_quant_matvec_into(
                 weights.handle, C.c_void_p(x_ptr), C.c_void_p(add_ptr or None), C.c_void_p(y_ptr), batch, C.c_void_p(stream or None)

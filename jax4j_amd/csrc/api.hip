@@ -781,7 +781,9 @@ int j4q_quant_matvec_into(j4q_buffer wh, const float *x, const float *add, float
     if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatvec_into", &w))) return rc;
     const int64_t N = w->dims[0], K = w->dims[1];
     const j4q::QMat m = qmat_of(*w);
-    if (add && add < y + batch * N && y < add + batch * N && !j4q::gemv_in_place_ok(w->qtype, m, batch))
+    if (add && add != y && add < y + batch * N && y < add + batch * N)
+        return fail(J4Q_EUNSUPPORTED, "quantMatvec_into: add overlaps y without being y itself");
+    if (add == y && !j4q::gemv_in_place_ok(w->qtype, m, batch))
         return fail(J4Q_EUNSUPPORTED,
                     "quantMatvec_into: an add that overlaps y needs cols <= %lld (one column window) or batch >= 3 on "
                     "Q4_0/Q8_0/Q4_K/Q6_K, got cols %lld, batch %lld",

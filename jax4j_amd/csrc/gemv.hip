@@ -53,8 +53,9 @@ int g_cus = 256;
 //    registers), else 8;
 //  - 9..16 rows: 4 waves of 8 blocks, windows of 32 blocks (1024 columns, a 64 KB x image,
 //    two workgroups per CU). Measured on the B = 16 decode step (all windows of a matrix in
-//    one launch): 3.41 ms at 4 waves, 3.42 ms at 8 (2048-column windows); either way a CU
-//    holds 8 waves, the LDS the x images take.
+//    one launch): 3.41 ms at 4 waves, 3.42 ms at 8 (2048-column windows), where a CU holds
+//    8 waves either way; 8 waves of 4 blocks over the same 1024-column windows (16 waves per
+//    CU) took 3.02 ms against 2.69 ms for 4 waves of 8.
 template <int FMT, int BB>
 constexpr int mfma_waves() { return BB > 8 ? 4 : (FMT == Q8_0 || FMT == Q4_0) ? 16 : 8; }
 template <int FMT, int BB>
@@ -101,16 +102,20 @@ hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y
     mfma_windows<FMT, BB>(m, windows, per);
     const uint64_t need = windows > 1 ? (uint64_t)windows * (uint64_t)b * (uint64_t)m.rows * 4u : 0;
     if (windows == 1 || (ws.ptr && ws.bytes >= need)) {
-        // workgroups resident at once (LDS-bound), shared out between the windows
+        // workgroups resident at once (LDS-bound), shared out between the windows; rounded
+        // down, since a workgroup past the resident count would start only when another one
+        // ends and double the launch's time (4096 x 14336 Q6_K at B = 16: 518 workgroups for
+        // 512 slots took 31 us)
         constexpr int lds = gmf::Plan<BB, gmf::Fmt<FMT>::GROUPS, W, IPW * S, gmf::round_tiles<BB, W>()>::kBytes;
         constexpr int per_cu = 163840 / lds > 0 ? 163840 / lds : 1;
-        int grid = (g_cus * (per_cu < 8 ? per_cu : 8) + windows - 1) / windows;
+        int grid = g_cus * (per_cu < 8 ? per_cu : 8) / windows;
+        if (grid < 1) grid = 1;
         if (grid > tiles) grid = tiles;
         hipError_t e = gmf::launch_k<FMT, BB, W, IPW, false, mfma_ring<FMT, BB>()>(m, x, windows == 1 ? add : nullptr, y, b, grid, s, 0, per,
                                                                 nb, nullptr, windows, ws.ptr);
         if (e != hipSuccess || windows == 1) return e;
         const int64_t n = (int64_t)b * m.rows;
-        const int64_t blocks = (n + 255) / 256;
+        const int64_t blocks = ((n % 4 == 0 ? n / 4 : n) + 255) / 256;  // a thread per float4 where n allows
         gmf::sum_windows_kernel<<<(unsigned)(blocks < 2048 ? blocks : 2048), 256, 0, s>>>(ws.ptr, windows, n, add, y);
         return hipGetLastError();
     }

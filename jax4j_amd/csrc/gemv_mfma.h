@@ -154,7 +154,8 @@ struct Fmt<Q6_K> {
 
 // LDS plan for BB batch rows, WAVES waves of NBW blocks each, rounds of RT tiles (byte
 // offsets):
-//   xa   [WAVES * NBW][2 BB rows][4 lane groups][16 B]   hi/lo fp16 x image
+//   xa   [WAVES * NBW][4 lane groups][2 BB rows][16 B]   hi/lo fp16 x image (a lane group's
+//        16 lanes read 16 consecutive 16-byte rows: no LDS bank conflicts)
 //   zero 512 BB bytes of zeros (A rows with no batch row read here, stride 0; none at
 //        BB = 16, where every row carries one)
 //   cin  [WAVES * NBW][G][BB] f32                         MFMA C input per block
@@ -218,166 +219,31 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
     const int blkw = kb0 + lw;     // ... and its first block in the row
     const Rsrc rs = gemv::rsrc_of(m, FMT);
 
-    // ---- 1. x image of this wave's slice, built before any weight load is issued --------
-    // Weight loads block at issue once the memory queues are full; anything queued behind
-    // them in a wave (such as this prologue) would wait for the whole stream. So each wave
-    // first turns its own slice of x into MFMA operands, with its own power-of-two scale per
-    // batch row (applied again when its partial sums are written), and needs no barrier.
+    // ---- 1. x loads, then the first tiles' weight loads, then the x image ----------------
+    // Each wave turns its own slice of x into MFMA operands, with its own power-of-two scale
+    // per batch row (applied again when its partial sums are written), and needs no barrier.
+    // The x loads go out first and the first TS tiles' weight loads right behind them, so
+    // the weight stream starts while the image is built (the image waits only for x: loads
+    // complete in issue order for the counter).
     constexpr int UNITS = BB * 4;                 // (batch row, lane group) units per block
+    static_assert(64 % UNITS == 0, "a lane's units share one batch row");
     constexpr int XPL = (NBW * UNITS + 63) / 64;  // units per lane
+    const int xb = (lane % UNITS) >> 2, xg = lane & 3;  // the batch row and lane group of this lane's units
     f32x4 xv[XPL][2];
     {
         const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint64_t)B * (uint64_t)K * 4u);
 #pragma unroll
         for (int i = 0; i < XPL; i++) {
-            const int u = lane + 64 * i;
-            const int bl = u / UNITS, rem = u - bl * UNITS, b = rem >> 2, gg = rem & 3;
-            const bool ok = u < NBW * UNITS && b < B && blkw + bl < nb;
-            const uint32_t off = (uint32_t)(b * K + (blkw + bl) * 32 + 4 * gg) * 4u;
+            const int bl = (lane + 64 * i) / UNITS;
+            const bool ok = lane + 64 * i < NBW * UNITS && xb < B && blkw + bl < nb;
+            const uint32_t off = (uint32_t)(xb * K + (blkw + bl) * 32 + 4 * xg) * 4u;
             xv[i][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? off : kOob, 0, 0));
             xv[i][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? off + 64u : kOob, 0, 0));
         }
     }
-    // zero block for the A rows and C inputs that carry no batch row (every wave writes the
-    // same zeros, so no wave depends on another)
-    if constexpr (!W16)
-        for (int i = lane; i < 128 * BB; i += 64) reinterpret_cast<uint32_t *>(lds + P::kZero)[i] = 0u;
-    float sx[BB];
-    int ex[BB];
-    {
-        float mx[BB];
-#pragma unroll
-        for (int b = 0; b < BB; b++) mx[b] = 0.f;
-#pragma unroll
-        for (int i = 0; i < XPL; i++) {
-            const int b = ((lane + 64 * i) % UNITS) >> 2;
-            const f32x4 a = xv[i][0], c = xv[i][1];
-            const float v = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                                  fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))));
-#pragma unroll
-            for (int bb = 0; bb < BB; bb++) mx[bb] = (b == bb) ? fmaxf(mx[bb], v) : mx[bb];
-        }
-#pragma unroll
-        for (int bb = 0; bb < BB; bb++) {
-            float v = mx[bb];
-            v = fmaxf(v, gemv::dpp<0xB1>(v));
-            v = fmaxf(v, gemv::dpp<0x4E>(v));
-            v = fmaxf(v, gemv::dpp<0x141>(v));
-            v = fmaxf(v, gemv::dpp<0x140>(v));
-            v = fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)),
-                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16))),
-                      fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)),
-                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48))));
-            // 2^e brings the slice maximum into [2^14, 2^15): no fp16 overflow, full precision
-            int e = 0;
-            if (v > 0.f && v <= 3.402823466e38f) {
-                int E;
-                (void)frexpf(v, &E);
-                e = 15 - E;
-                e = e < -126 ? -126 : (e > 127 ? 127 : e);
-            }
-            ex[bb] = e;
-            sx[bb] = ldexpf(1.0f, e);
-        }
-    }
-    {
-        uint8_t *xa = lds + P::kXa;
-        float *cin = reinterpret_cast<float *>(lds + P::kCin);
-#pragma unroll
-        for (int i = 0; i < XPL; i++) {
-            const int u = lane + 64 * i;
-            const int bl = u / UNITS, rem = u - bl * UNITS, b = rem >> 2, gg = rem & 3;
-            const int blk = lw + bl;  // x image index (window-relative)
-            float s = 0.f;
-#pragma unroll
-            for (int bb = 0; bb < BB; bb++) s = (b == bb) ? sx[bb] : s;
-            const f32x4 a = xv[i][0] * s, c = xv[i][1] * s;
-            const f32x4 hi4 = c * F::SIGMA;
-            // slots: 4g + {0, 2, 1, 3}, then 16 + 4g + {0, 2, 1, 3} times SIGMA
-            const float v[8] = {a.x, a.z, a.y, a.w, hi4.x, hi4.z, hi4.y, hi4.w};
-            uint32_t hw[4], lw[4];
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                const h2 h = __builtin_convertvector((f32x2{v[2 * p], v[2 * p + 1]}), h2);
-                const float r0 = v[2 * p] - (float)h.x, r1 = v[2 * p + 1] - (float)h.y;
-                const h2 l = __builtin_convertvector((f32x2{r0, r1}), h2);
-                hw[p] = __builtin_bit_cast(uint32_t, h);
-                lw[p] = __builtin_bit_cast(uint32_t, l);
-            }
-            // block sums of x' over elements 0..15 and 16..31 (this unit's 4 + 4, then the quad)
-            float s0 = (a.x + a.y) + (a.z + a.w), s1 = (c.x + c.y) + (c.z + c.w);
-            s0 += gemv::dpp<0xB1>(s0);
-            s0 += gemv::dpp<0x4E>(s0);
-            s1 += gemv::dpp<0xB1>(s1);
-            s1 += gemv::dpp<0x4E>(s1);
-            if (u < NBW * UNITS) {
-                *reinterpret_cast<u32x4 *>(xa + ((blk * 2 * BB + b) * 4 + gg) * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
-                *reinterpret_cast<u32x4 *>(xa + ((blk * 2 * BB + BB + b) * 4 + gg) * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
-                if (gg == 0) {
-                    constexpr float U = 5.9604644775390625e-8f;  // 2^-24
-                    if constexpr (G == 2) {
-                        cin[(blk * 2 + 0) * BB + b] = -F::OFF * U * s0;
-                        cin[(blk * 2 + 1) * BB + b] = -F::OFF * U * s1;
-                    } else if constexpr (FMT == Q4_K) {
-                        cin[blk * BB + b] = U * (s0 + s1);
-                    } else {
-                        cin[blk * BB + b] = -F::OFF * U * (s0 + s1);
-                    }
-                }
-            }
-        }
-    }
-    // The slice was written by this wave only; LDS operations of one wave complete in order,
-    // so waiting for them is all the ordering the reads below need.
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-
-    // Lane (m, g) of the A operand: rows m < BB are hi of batch row m, rows 8..8+BB-1 lo of
-    // batch row m - 8, other rows read the zero block with stride 0. The C rows of lane
-    // group g are 4g..4g+3: groups 0 and 1 hold the hi rows of batch rows 4 (g & 1) + j and
-    // take the C inputs; groups 2 and 3 hold the lo rows and read zeros.
-    // BB = 16: row m of the first A operand is hi of batch row m, of the second lo of batch
-    // row m; the second MFMA takes the first one's result as its C input, so every C row
-    // 4g + j is batch row 4g + j (hi + lo) and every lane group takes the C inputs.
-    const int mrow = lane & 15;
-    int abase, astride;
-    if constexpr (W16) {
-        abase = P::kXa + ((lw * 2 * BB + mrow) * 4 + g) * 16;
-        astride = 128 * BB;
-    } else if (mrow < BB) {
-        abase = P::kXa + ((lw * 2 * BB + mrow) * 4 + g) * 16;
-        astride = 128 * BB;
-    } else if (mrow >= 8 && mrow < 8 + BB) {
-        abase = P::kXa + ((lw * 2 * BB + BB + mrow - 8) * 4 + g) * 16;
-        astride = 128 * BB;
-    } else {
-        abase = P::kZero + g * 16;
-        astride = 0;
-    }
-    constexpr int JB = BB < 4 ? BB : 4;  // C rows per lane that carry a batch row
-    const int hb = W16 ? 4 * g : 4 * (g & 1);  // first batch row of this lane's C rows
-    const bool hi_lane = W16 || (g < 2 && hb < BB);
-    const int cbase = hi_lane ? P::kCin + (lw * G * BB + hb) * 4 : P::kZero;
-    const int cstride = hi_lane ? G * BB * 4 : 0;
-    auto a_op = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + bl * astride); };
-    // BB = 16: the lo operand, BB rows further on in the block's image
-    auto a_lo = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + BB * 64 + bl * astride); };
-    auto c_in = [&](int bl, int k) { return reinterpret_cast<const float *>(lds + cbase + bl * cstride)[k]; };
-    // registers keep only this lane's C inputs: k = j (group 0) and k = BB + j (Q6_K group 1)
-    h8 areg[XREG ? NBW : 1];
-    float creg[XREG ? NBW : 1][G * JB];
-    if constexpr (XREG) {
-#pragma unroll
-        for (int bl = 0; bl < NBW; bl++) {
-            areg[bl] = a_op(bl);
-#pragma unroll
-            for (int kk = 0; kk < G * JB; kk++) creg[bl][kk] = c_in(bl, kk < JB ? kk : BB + kk - JB);
-        }
-    }
-
-    // ---- 2. weight loads of the first two tiles -----------------------------------------
-    // The reducing threads (b, nn) = (tid / 16, tid % 16), tid < 16 BB, also fetch prev[b][row]
-    // and add[b][row] with the tile's weights, so waiting for them never drains the loads
-    // issued later.
+    // Weight loads of the first TS tiles. The reducing threads (b, nn) = (tid / 16, tid % 16),
+    // tid < 16 BB, also fetch prev[b][row] and add[b][row] with the tile's weights, so waiting
+    // for them never drains the loads issued later.
     const __amdgpu_buffer_rsrc_t addr = make_rsrc(add ? (const void *)add : (const void *)y, add ? (uint64_t)B * N * 4u : 0);
     const __amdgpu_buffer_rsrc_t prevr = make_rsrc(prev ? (const void *)prev : (const void *)y, prev ? (uint64_t)B * N * 4u : 0);
     const int rb = (int)threadIdx.x >> 4, rn = (int)threadIdx.x & 15;
@@ -428,12 +294,141 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
 #pragma unroll
     for (int k = 0; k < TS; k++) load_tile(tset[k], avs[k], t0 + k * tstep);
     __builtin_amdgcn_sched_barrier(0);
+    // zero block for the A rows and C inputs that carry no batch row (every wave writes the
+    // same zeros, so no wave depends on another)
+    if constexpr (!W16)
+        for (int i = lane; i < 128 * BB; i += 64) reinterpret_cast<uint32_t *>(lds + P::kZero)[i] = 0u;
+    // 2^e brings the maximum of |x| over the slice and the batch row into [2^14, 2^15): no
+    // fp16 overflow, full precision. The lanes of a batch row are its quad and the lanes
+    // 16, 32 or 48 further on (UNITS apart).
+    int ex;
+    float sx;
+    {
+        float v = 0.f;
+#pragma unroll
+        for (int i = 0; i < XPL; i++) {
+            const f32x4 a = xv[i][0], c = xv[i][1];
+            v = fmaxf(v, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                               fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w)))));
+        }
+        v = fmaxf(v, gemv::dpp<0xB1>(v));
+        v = fmaxf(v, gemv::dpp<0x4E>(v));
+        if constexpr (UNITS <= 32) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
+            v = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+        }
+        if constexpr (UNITS <= 16) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
+            v = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+        }
+        int e = 0;
+        if (v > 0.f && v <= 3.402823466e38f) {
+            int E;
+            (void)frexpf(v, &E);
+            e = 15 - E;
+            e = e < -126 ? -126 : (e > 127 ? 127 : e);
+        }
+        ex = e;
+        sx = ldexpf(1.0f, e);
+    }
+    {
+        uint8_t *xa = lds + P::kXa;
+        float *cin = reinterpret_cast<float *>(lds + P::kCin);
+#pragma unroll
+        for (int i = 0; i < XPL; i++) {
+            const int u = lane + 64 * i;
+            const int bl = u / UNITS, b = xb, gg = xg;
+            const int blk = lw + bl;  // x image index (window-relative)
+            const f32x4 a = xv[i][0] * sx, c = xv[i][1] * sx;
+            const f32x4 hi4 = c * F::SIGMA;
+            // slots: 4g + {0, 2, 1, 3}, then 16 + 4g + {0, 2, 1, 3} times SIGMA
+            const float v[8] = {a.x, a.z, a.y, a.w, hi4.x, hi4.z, hi4.y, hi4.w};
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const h2 h = __builtin_convertvector((f32x2{v[2 * p], v[2 * p + 1]}), h2);
+                const float r0 = v[2 * p] - (float)h.x, r1 = v[2 * p + 1] - (float)h.y;
+                const h2 l = __builtin_convertvector((f32x2{r0, r1}), h2);
+                hw[p] = __builtin_bit_cast(uint32_t, h);
+                lw[p] = __builtin_bit_cast(uint32_t, l);
+            }
+            // block sums of x' over elements 0..15 and 16..31 (this unit's 4 + 4, then the quad)
+            float s0 = (a.x + a.y) + (a.z + a.w), s1 = (c.x + c.y) + (c.z + c.w);
+            s0 += gemv::dpp<0xB1>(s0);
+            s0 += gemv::dpp<0x4E>(s0);
+            s1 += gemv::dpp<0xB1>(s1);
+            s1 += gemv::dpp<0x4E>(s1);
+            if (u < NBW * UNITS) {
+                *reinterpret_cast<u32x4 *>(xa + ((blk * 4 + gg) * 2 * BB + b) * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4 *>(xa + ((blk * 4 + gg) * 2 * BB + BB + b) * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                if (gg == 0) {
+                    constexpr float U = 5.9604644775390625e-8f;  // 2^-24
+                    if constexpr (G == 2) {
+                        cin[(blk * 2 + 0) * BB + b] = -F::OFF * U * s0;
+                        cin[(blk * 2 + 1) * BB + b] = -F::OFF * U * s1;
+                    } else if constexpr (FMT == Q4_K) {
+                        cin[blk * BB + b] = U * (s0 + s1);
+                    } else {
+                        cin[blk * BB + b] = -F::OFF * U * (s0 + s1);
+                    }
+                }
+            }
+        }
+    }
+    // The slice was written by this wave only; LDS operations of one wave complete in order,
+    // so waiting for them is all the ordering the reads below need.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+
+    // Lane (m, g) of the A operand: rows m < BB are hi of batch row m, rows 8..8+BB-1 lo of
+    // batch row m - 8, other rows read the zero block with stride 0. The C rows of lane
+    // group g are 4g..4g+3: groups 0 and 1 hold the hi rows of batch rows 4 (g & 1) + j and
+    // take the C inputs; groups 2 and 3 hold the lo rows and read zeros.
+    // BB = 16: row m of the first A operand is hi of batch row m, of the second lo of batch
+    // row m; the second MFMA takes the first one's result as its C input, so every C row
+    // 4g + j is batch row 4g + j (hi + lo) and every lane group takes the C inputs.
+    const int mrow = lane & 15;
+    int abase, astride;
+    if constexpr (W16) {
+        abase = P::kXa + ((lw * 4 + g) * 2 * BB + mrow) * 16;
+        astride = 128 * BB;
+    } else if (mrow < BB) {
+        abase = P::kXa + ((lw * 4 + g) * 2 * BB + mrow) * 16;
+        astride = 128 * BB;
+    } else if (mrow >= 8 && mrow < 8 + BB) {
+        abase = P::kXa + ((lw * 4 + g) * 2 * BB + BB + mrow - 8) * 16;
+        astride = 128 * BB;
+    } else {
+        abase = P::kZero + g * 16;
+        astride = 0;
+    }
+    constexpr int JB = BB < 4 ? BB : 4;  // C rows per lane that carry a batch row
+    const int hb = W16 ? 4 * g : 4 * (g & 1);  // first batch row of this lane's C rows
+    const bool hi_lane = W16 || (g < 2 && hb < BB);
+    const int cbase = hi_lane ? P::kCin + (lw * G * BB + hb) * 4 : P::kZero;
+    const int cstride = hi_lane ? G * BB * 4 : 0;
+    auto a_op = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + bl * astride); };
+    // BB = 16: the lo operand, BB rows further on in the lane group's image
+    auto a_lo = [&](int bl) { return *reinterpret_cast<const h8 *>(lds + abase + BB * 16 + bl * astride); };
+    auto c_in = [&](int bl, int k) { return reinterpret_cast<const float *>(lds + cbase + bl * cstride)[k]; };
+    // registers keep only this lane's C inputs: k = j (group 0) and k = BB + j (Q6_K group 1)
+    h8 areg[XREG ? NBW : 1];
+    float creg[XREG ? NBW : 1][G * JB];
+    if constexpr (XREG) {
+#pragma unroll
+        for (int bl = 0; bl < NBW; bl++) {
+            areg[bl] = a_op(bl);
+#pragma unroll
+            for (int kk = 0; kk < G * JB; kk++) creg[bl][kk] = c_in(bl, kk < JB ? kk : BB + kk - JB);
+        }
+    }
+
     // per-batch-row factor that undoes this wave's x scale (2^-e); the 2^24 of the weights is
     // applied as a separate exact product, since 2^(24 - e) overflows for a slice maximum
     // of 2^118 or more (e <= -104)
+    // (batch row bb's exponent is that of lane 4 bb)
     float wscale[BB];
 #pragma unroll
-    for (int bb = 0; bb < BB; bb++) wscale[bb] = ldexpf(1.0f, -ex[bb]);
+    for (int bb = 0; bb < BB; bb++) wscale[bb] = ldexpf(1.0f, -__builtin_amdgcn_readlane(ex, 4 * bb));
 
     auto A = [&](int bl) -> h8 {
         if constexpr (XREG) return areg[bl];
@@ -672,10 +667,33 @@ hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, i
 
 // y[i] = ((part[0][i] + part[1][i]) + ...) + add[i] for i < n (= B x rows): the windows'
 // sums in window order (the same additions as windows chained through prev), then the add
-// on its own. Each element is read and written by one thread, so add may be y itself.
+// on its own. Each element is read and written by one thread, so add may be y itself. A
+// thread takes 4 consecutive elements (one element when n or an address does not allow
+// float4 access) and issues the loads of up to 8 windows before it adds any of them, so the
+// latencies overlap instead of adding up window by window.
 __global__ void __launch_bounds__(256)
 sum_windows_kernel(const float *__restrict__ part, int windows, int64_t n, const float *add, float *y) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    // vector path for whole float4 rows at 16-byte aligned addresses
+    const bool vec = (n & 3) == 0 && (((uintptr_t)part | (uintptr_t)add | (uintptr_t)y) & 15u) == 0;
+    const int64_t n4 = vec ? n / 4 : 0;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+        // add is fetched with the first windows (it is added last)
+        const f32x4 a = add ? reinterpret_cast<const f32x4 *>(add)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 v = reinterpret_cast<const f32x4 *>(part)[i];
+        for (int r0 = 1; r0 < windows; r0 += 8) {
+            f32x4 t[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (r0 + k < windows) t[k] = reinterpret_cast<const f32x4 *>(part + (int64_t)(r0 + k) * n)[i];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (r0 + k < windows) v += t[k];
+        }
+        if (add) v += a;
+        reinterpret_cast<f32x4 *>(y)[i] = v;
+    }
+    for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
         float v = part[i];
         for (int r = 1; r < windows; r++) v += part[(int64_t)r * n + i];
         if (add) v += add[i];

@@ -273,24 +273,26 @@ def test_gemv_batched_wide_k(backend, uploaded, qt, rows, cols, B):
 
 @pytest.mark.parametrize("cols", [4096, 11008])
 @pytest.mark.parametrize("B", [8, 16])
-def test_gemv_batched_add_in_place(backend, uploaded, cols, B):
+@pytest.mark.parametrize("shift", [0, 1])
+def test_gemv_batched_add_in_place(backend, uploaded, cols, B, shift):
     """quantMatvecAdd with y on the add buffer itself (a residual updated in place). The
     column windows' partial sums meet in a workspace and one kernel adds them and then add,
     element by element, so the in-place call runs the same launches as the out-of-place one
-    and gives the same bits."""
+    and gives the same bits. shift = 1 puts y 4 bytes past a 16-byte boundary (the window
+    sums then take their one-element path)."""
     qt, rows = QuantType.Q4_0, 1000
-    note("batched in-place add", qt.name, rows, cols, "B", B)
+    note("batched in-place add", qt.name, rows, cols, "B", B, "shift", shift)
     blob, w = uploaded(qt, rows, cols)
     xs = S.activations_f32(rows + 3, B * cols).reshape(B, cols)
     add = S.activations_f32(rows + 4, B * rows).reshape(B, rows)
     xb = backend.upload(xs, shape=(B, cols))
     ab = backend.upload(add, shape=(B, rows))
     ref = backend.download(backend.quant_matvec_add(w, xb, ab)).reshape(B, rows)
-    res = backend.upload(add, shape=(B, rows))
-    rp = backend.buffer_desc(res).device_ptr
+    res = backend.upload(np.concatenate([np.zeros(shift, np.float32), add.reshape(-1)]))
+    rp = backend.buffer_desc(res).device_ptr + 4 * shift
     backend.quant_matvec_into(w, backend.buffer_desc(xb).device_ptr, rp, rp, B)
     backend.sync()
-    got = backend.download(res).reshape(B, rows)
+    got = backend.download(res)[shift:].reshape(B, rows)
     assert np.array_equal(bits(got), bits(ref))
     for b in range(B):
         y64 = oracle.matvec_f64(qt.id, blob, rows, cols, xs[b]) + add[b].astype(np.float64)
@@ -494,5 +496,20 @@ def test_in_place_add_wider_than_one_window_is_rejected(backend, uploaded):
     rp = backend.buffer_desc(res).device_ptr
     with pytest.raises(IllegalArgumentException, match="overlaps y"):
         backend.quant_matvec_into(w, backend.buffer_desc(x).device_ptr, rp, rp, 1)
+    backend.release(x)
+    backend.release(res)
+
+
+def test_add_partly_overlapping_y_is_rejected(backend, uploaded):
+    """An add that overlaps y without being y itself would be read by one thread while
+    another rewrites it, so the stream-ordered entry point refuses it at any size."""
+    qt, rows, cols = QuantType.Q4_0, 24, 512
+    blob, w = uploaded(qt, rows, cols)
+    x = backend.upload(S.activations_f32(6, 4 * cols))
+    res = backend.upload(np.zeros(4 * rows + 4, np.float32))
+    rp = backend.buffer_desc(res).device_ptr
+    for B in (1, 4):
+        with pytest.raises(IllegalArgumentException, match="without being y itself"):
+            backend.quant_matvec_into(w, backend.buffer_desc(x).device_ptr, rp + 16, rp, B)
     backend.release(x)
     backend.release(res)
