@@ -297,6 +297,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// W-tile swizzle of gemm_bf16_lds: 16-byte chunk c of row r sits at slot c ^ wswz(r). Bits
+// 1..3 of the row spread the 16 rows of one operand read over all banks; bit 4 moves rows 16
+// apart by 64 bytes, so a wave's reads of two column tiles (rows r and r + 16) never share
+// banks and never sit a constant offset apart (the compiler merged those into one
+// ds_read2st64_b64 whose two halves conflicted: 2.2 M bank-conflict cycles per 128 x 128
+// launch at M = 2048).
+__device__ __forceinline__ int wswz(int row) { return ((row >> 1) & 7) ^ (((row >> 4) & 1) << 2); }
+
 // Prefill GEMM, bf16 variant for even N from M = 65 on (whenever its grid has at least 128
 // workgroups; launch_gemm_q8_bf16 in gemm.hip picks the tile), results bit-identical to
 // gemm_bf16_wide (the same blocks go to the same waves in the same order):
@@ -305,7 +313,7 @@ __device__ __forceinline__ void lds_barrier() {
 //  - Every stage moves straight from global memory into one of three LDS stage buffers:
 //    X as BM rows x 256 bytes (16-byte chunk c of row r at c ^ (r % 16): the 16 rows of an
 //    operand read fall on distinct banks), W as BN rows x 128 bytes (chunk c of row r at
-//    c ^ ((r / 2) % 8)), and each wave's scales of the stage into its own 256-byte slot.
+//    c ^ wswz(r)), and each wave's scales of the stage into its own 256-byte slot.
 //    Each wave's LDS loads pick the global chunk that belongs at their lane's LDS slot.
 //  - The buffers are separate __shared__ arrays and the ring is unrolled by three, so the
 //    compiler knows which loads write the buffer a read touches and adds no waits of its
@@ -355,13 +363,13 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
         xk[j] = c * 8;
     }
     // W load j covers rows 8 (8 j + wave) .. +7; slot L % 8 of row 8 (8 j + wave) + L / 8
-    // holds chunk (L % 8) ^ ((row / 2) % 8).
+    // holds chunk (L % 8) ^ wswz(row).
     const __amdgpu_buffer_rsrc_t wq = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
     uint32_t woff[NJ];
     int wk[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int row = 8 * (8 * j + wave) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7), n = n0 + row;
+        const int row = 8 * (8 * j + wave) + (lane >> 3), c = (lane & 7) ^ wswz(row), n = n0 + row;
         woff[j] = n < N ? (uint32_t)n * (uint32_t)K + (uint32_t)c * 16u : kOob;
         wk[j] = c * 16;
     }
@@ -400,8 +408,8 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
     // Stage in (xb, wb, db) and the loads of stage inext into (xn, wn, dn).
     // A operand of row tile t, block b: row 16 t + m16, chunk 4 (2 b + kh) + g, at slot
     // chunk ^ m16. B operand of column tile j: row 16 NJ nw + 16 j + m16, bytes
-    // 32 (2 b + kh) + 8 g, i.e. chunk 2 (2 b + kh) + g / 2 at slot chunk ^ ((row / 2) % 8),
-    // half g % 2.
+    // 32 (2 b + kh) + 8 g, i.e. chunk 2 (2 b + kh) + g / 2 at slot chunk ^ wswz(row), half
+    // g % 2.
     auto stage = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *db, int inext, uint8_t *xn, uint8_t *wn,
                      uint8_t *dn) {
         if (!ILV) {
@@ -418,7 +426,7 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const int row = 16 * NJ * nw + 16 * j + m16, cb = 2 * (2 * bb + kh) + (g >> 1);
-                const u32x2 q = *reinterpret_cast<const u32x2 *>(wb + row * 128 + ((cb ^ ((row >> 1) & 7)) << 4) + 8 * (g & 1));
+                const u32x2 q = *reinterpret_cast<const u32x2 *>(wb + row * 128 + ((cb ^ wswz(row)) << 4) + 8 * (g & 1));
                 const uint32_t dbits = *reinterpret_cast<const uint16_t *>(db + wave * 256 + (bb * 16 * NJ + 16 * j + m16) * 2);
                 b[bb][j] = dequant8(q, half_bits_to_float(dbits));
             }
