@@ -81,6 +81,39 @@ void mfma_windows(const QMat &m, int &windows, int &per) {
     windows = (nb + per - 1) / per;
 }
 
+// Workgroups of launch_mfma<FMT, BB>'s kernel that one CU holds at once, by LDS and by
+// registers (hipOccupancyMaxActiveBlocksPerMultiprocessor at init); the LDS bound alone
+// would launch two workgroups per CU where registers admit one (Q4_K with 8 waves of ~170
+// VGPRs at 4 rows, Q4_0 with 16 waves of ~100), and the second half of the grid would run
+// only after the first.
+int g_mfma_resident[4][3];  // [Q4_0, Q8_0, Q4_K, Q6_K][BB 4, 8, 16]; 0 = not measured
+
+constexpr int fmt_slot(int fmt) { return fmt == Q4_0 ? 0 : fmt == Q8_0 ? 1 : fmt == Q4_K ? 2 : 3; }
+constexpr int bb_slot(int bb) { return bb <= 4 ? 0 : bb <= 8 ? 1 : 2; }
+
+template <int FMT, int BB>
+constexpr int mfma_lds() {
+    return gmf::Plan<BB, gmf::Fmt<FMT>::GROUPS, mfma_waves<FMT, BB>(), mfma_ipw<FMT, BB>() * (FMT == Q8_0 ? 2 : 4),
+                     gmf::round_tiles<BB, mfma_waves<FMT, BB>()>()>::kBytes;
+}
+
+template <int FMT, int BB>
+void measure_resident() {
+    constexpr int W = mfma_waves<FMT, BB>();
+    int n = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &n, (const void *)gmf::gemv_mfma_kernel<FMT, BB, W, mfma_ipw<FMT, BB>(), false, mfma_ring<FMT, BB>()>, W * 64,
+        mfma_lds<FMT, BB>());
+    g_mfma_resident[fmt_slot(FMT)][bb_slot(BB)] = e == hipSuccess && n > 0 ? n : 0;
+}
+
+template <int FMT>
+void measure_resident_fmt() {
+    measure_resident<FMT, 4>();
+    measure_resident<FMT, 8>();
+    measure_resident<FMT, 16>();
+}
+
 // Batched GEMV on the matrix cores (gemv_mfma.h) for up to 16 batch rows per launch,
 // persistent workgroups of 16-row tiles, each launch window of up to 128 blocks (4096
 // columns; 64 at 16 rows) split into one slice per wave. A wider K has several windows:
@@ -102,12 +135,13 @@ hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y
     mfma_windows<FMT, BB>(m, windows, per);
     const uint64_t need = windows > 1 ? (uint64_t)windows * (uint64_t)b * (uint64_t)m.rows * 4u : 0;
     if (windows == 1 || (ws.ptr && ws.bytes >= need)) {
-        // workgroups resident at once (LDS-bound), shared out between the windows; rounded
-        // down, since a workgroup past the resident count would start only when another one
-        // ends and double the launch's time (4096 x 14336 Q6_K at B = 16: 518 workgroups for
-        // 512 slots took 31 us)
-        constexpr int lds = gmf::Plan<BB, gmf::Fmt<FMT>::GROUPS, W, IPW * S, gmf::round_tiles<BB, W>()>::kBytes;
-        constexpr int per_cu = 163840 / lds > 0 ? 163840 / lds : 1;
+        // workgroups resident at once, shared out between the windows; rounded down, since a
+        // workgroup past the resident count would start only when another one ends and double
+        // the launch's time (4096 x 14336 Q6_K at B = 16: 518 workgroups for 512 slots took
+        // 31 us)
+        constexpr int lds = mfma_lds<FMT, BB>();
+        const int measured = g_mfma_resident[fmt_slot(FMT)][bb_slot(BB)];
+        const int per_cu = measured > 0 ? measured : (163840 / lds > 0 ? 163840 / lds : 1);
         int grid = g_cus * (per_cu < 8 ? per_cu : 8) / windows;
         if (grid < 1) grid = 1;
         if (grid > tiles) grid = tiles;
@@ -195,7 +229,13 @@ hipError_t launch_valu(int id, const QMat &m, const float *x, const float *add, 
 
 }  // namespace
 
-void gemv_set_cus(int cus) { g_cus = cus > 0 ? cus : 256; }
+void gemv_set_cus(int cus) {
+    g_cus = cus > 0 ? cus : 256;
+    measure_resident_fmt<Q4_0>();
+    measure_resident_fmt<Q8_0>();
+    measure_resident_fmt<Q4_K>();
+    measure_resident_fmt<Q6_K>();
+}
 
 bool gemv_in_place_ok(int id, const QMat &m, int64_t batch) {
     return m.cols <= gemv::kMaxWindow || (batch >= 3 && mfma_format(id, m));
