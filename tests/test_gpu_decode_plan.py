@@ -7,6 +7,11 @@ h = down.x_down + h', then logits = head.h, replayed as one captured HIP graph
 as the single calls, so its outputs equal the eager composition bit for bit; against the
 fp64 oracle chain the fp32 residual stream adds its roundings, bound 1e-4 * ||ref||_inf
 (10x inside the 1e-3 decode tolerance).
+
+A second, wider model gives every batched GEMV several column windows (K above 1024 columns
+at 9-16 batch rows, above 4096 at 3-8, all four formats), whose sums meet in a second launch
+on the plan's own workspace in the plan and on stream-ordered memory in the single calls:
+the two agree bit for bit, on every replay (the workspace is reused by every GEMV of a step).
 """
 from __future__ import annotations
 
@@ -25,14 +30,24 @@ from jax4j_amd.backend import DecodePlan
 pytestmark = pytest.mark.gpu
 
 Q4K, Q6K, Q8, Q40 = QuantType.Q4_K, QuantType.Q6_K, QuantType.Q8_0, QuantType.Q4_0
-D, QR, KVR, FFN, VOCAB = 512, 512, 256, 1024, 1000
+
+
+class Dims:
+    def __init__(self, d, qr, kvr, ffn, vocab):
+        self.D, self.QR, self.KVR, self.FFN, self.VOCAB = d, qr, kvr, ffn, vocab
+        self.shapes = dict(q=(qr, d), k=(kvr, d), v=(kvr, d), o=(d, qr), gate=(ffn, d), up=(ffn, d), down=(d, ffn))
+
+
+SMALL = Dims(512, 512, 256, 1024, 1000)
+# every batched GEMV over several column windows: K = 1536 (q|k|v, gate|up, head) and 4352
+# (down) have 2 and 5 windows at 16 rows, down 2 at 3-8 rows
+WIDE = Dims(1536, 1536, 512, 4352, 1000)
 # layer 0: one type per group (q|k|v and gate|up fused into one launch each); layer 1: v and
 # up of other types (runs launched separately, outputs copied into the fused layout)
 TYPES = [
     dict(q=Q4K, k=Q4K, v=Q4K, o=Q4K, gate=Q4K, up=Q4K, down=Q6K),
     dict(q=Q4K, k=Q4K, v=Q6K, o=Q40, gate=Q4K, up=Q8, down=Q6K),
 ]
-SHAPES = dict(q=(QR, D), k=(KVR, D), v=(KVR, D), o=(D, QR), gate=(FFN, D), up=(FFN, D), down=(D, FFN))
 
 
 def bits(a):
@@ -52,31 +67,48 @@ def ptr(backend, buf):
     return backend.buffer_desc(buf).device_ptr
 
 
-@pytest.fixture(scope="module")
-def model(backend):
+def build_model(backend, dims, seed):
     """Two layers of weights and a head (host blobs kept for the oracle)."""
     layers, blobs = [], []
-    seed = 0xD0C
     for types in TYPES:
         lw, lb = {}, {}
         for name, qt in types.items():
-            rows, cols = SHAPES[name]
+            rows, cols = dims.shapes[name]
             blob = S.quant_blocks(qt, seed, rows, cols)
             seed += 1
             lb[name] = (qt, blob)
             lw[name] = backend.upload_quantized(blob, qt, (rows, cols))
         layers.append(lw)
         blobs.append(lb)
-    hblob = S.quant_blocks(Q6K, seed, VOCAB, D)
-    head = backend.upload_quantized(hblob, Q6K, (VOCAB, D))
-    yield layers, blobs, head, hblob
+    hblob = S.quant_blocks(Q6K, seed, dims.VOCAB, dims.D)
+    head = backend.upload_quantized(hblob, Q6K, (dims.VOCAB, dims.D))
+    return layers, blobs, head, hblob
+
+
+def release_model(backend, m):
+    layers, _, head, _ = m
     for lw in layers:
         for w in lw.values():
             backend.release(w)
     backend.release(head)
 
 
-def make_io(backend, B):
+@pytest.fixture(scope="module")
+def model(backend):
+    m = build_model(backend, SMALL, 0xD0C)
+    yield m
+    release_model(backend, m)
+
+
+@pytest.fixture(scope="module")
+def wide_model(backend):
+    m = build_model(backend, WIDE, 0xD1C)
+    yield m
+    release_model(backend, m)
+
+
+def make_io(backend, B, dims=SMALL):
+    D, QR, FFN, VOCAB = dims.D, dims.QR, dims.FFN, dims.VOCAB
     h0 = S.activations_f32(71 + B, B * D).reshape(B, D)
     xo = S.activations_f32(72 + B, B * QR).reshape(B, QR)
     xd = S.activations_f32(73 + B, B * FFN).reshape(B, FFN)
@@ -86,20 +118,20 @@ def make_io(backend, B):
         h0=backend.upload(h0, shape=(B, D)),
         x_o=backend.upload(xo, shape=(B, QR)),
         x_down=backend.upload(xd, shape=(B, FFN)),
-        qkv=backend.upload(np.zeros(L * B * (QR + 2 * KVR), np.float32)),
+        qkv=backend.upload(np.zeros(L * B * (QR + 2 * dims.KVR), np.float32)),
         gate_up=backend.upload(np.zeros(L * B * 2 * FFN, np.float32)),
         logits=backend.upload(np.zeros(B * VOCAB, np.float32)),
     )
     return h0, xo, xd, bufs
 
 
-def read(backend, bufs, B):
+def read(backend, bufs, B, dims=SMALL):
     L = len(TYPES)
     return (
-        backend.download(bufs["h"]).reshape(B, D),
-        backend.download(bufs["qkv"]).reshape(L, B, QR + 2 * KVR),
-        backend.download(bufs["gate_up"]).reshape(L, B, 2 * FFN),
-        backend.download(bufs["logits"]).reshape(B, VOCAB),
+        backend.download(bufs["h"]).reshape(B, dims.D),
+        backend.download(bufs["qkv"]).reshape(L, B, dims.QR + 2 * dims.KVR),
+        backend.download(bufs["gate_up"]).reshape(L, B, 2 * dims.FFN),
+        backend.download(bufs["logits"]).reshape(B, dims.VOCAB),
     )
 
 
@@ -133,7 +165,7 @@ def eager(backend, layers, head, h0, xo, xd):
     return h, np.stack(qkvs), np.stack(gus), mv(head, h)
 
 
-def oracle_chain(blobs, hblob, h0, xo, xd):
+def oracle_chain(blobs, hblob, h0, xo, xd, dims=SMALL):
     def mm(qb, x):
         qt, blob = qb
         rows, cols = blob_shape[id(blob)]
@@ -142,8 +174,8 @@ def oracle_chain(blobs, hblob, h0, xo, xd):
     blob_shape = {}
     for lb in blobs:
         for name, (qt, blob) in lb.items():
-            blob_shape[id(blob)] = SHAPES[name]
-    blob_shape[id(hblob)] = (VOCAB, D)
+            blob_shape[id(blob)] = dims.shapes[name]
+    blob_shape[id(hblob)] = (dims.VOCAB, dims.D)
     h = h0.astype(np.float64)
     qkvs, gus = [], []
     for lb in blobs:
@@ -155,11 +187,10 @@ def oracle_chain(blobs, hblob, h0, xo, xd):
     return h, np.stack(qkvs), np.stack(gus), mm((Q6K, hblob), h)
 
 
-@pytest.mark.parametrize("B", [1, 3, 16])
-def test_decode_plan_matches_eager_and_oracle(backend, model, B):
-    note("decode plan", "B", B)
-    layers, blobs, head, hblob = model
-    h0, xo, xd, bufs = make_io(backend, B)
+def check_plan(backend, m, B, dims):
+    layers, blobs, head, hblob = m
+    D, QR, KVR, FFN, VOCAB = dims.D, dims.QR, dims.KVR, dims.FFN, dims.VOCAB
+    h0, xo, xd, bufs = make_io(backend, B, dims)
     io = {k: ptr(backend, bufs[k]) for k in ("h", "x_o", "x_down", "qkv", "gate_up", "logits")}
     plan = backend.decode_plan(layers, head, B, io)
     info = plan.info()
@@ -167,11 +198,12 @@ def test_decode_plan_matches_eager_and_oracle(backend, model, B):
     assert (info["d_model"], info["qkv_rows"], info["ffn"], info["vocab"]) == (D, QR + 2 * KVR, FFN, VOCAB)
     # layer 0: q|k|v, o, gate|up, down = 4 GEMVs; layer 1: q|k, v, o, gate, up, down = 6; head 1
     assert info["gemvs_per_step"] == 11
-    total = sum(t.byte_size_for(SHAPES[n][0] * SHAPES[n][1]) for types in TYPES for n, t in types.items())
+    sh = dims.shapes
+    total = sum(t.byte_size_for(sh[n][0] * sh[n][1]) for types in TYPES for n, t in types.items())
     assert info["weight_bytes"] == total + Q6K.byte_size_for(VOCAB * D)
 
     ref_eager = eager(backend, layers, head, h0, xo, xd)
-    ref64 = oracle_chain(blobs, hblob, h0, xo, xd)
+    ref64 = oracle_chain(blobs, hblob, h0, xo, xd, dims)
     lib = N.load()
     first = None
     for replay in range(3):
@@ -179,7 +211,7 @@ def test_decode_plan_matches_eager_and_oracle(backend, model, B):
         assert lib.j4q_copy(C.c_void_p(io["h"]), C.c_void_p(ptr(backend, bufs["h0"])), B * D * 4, None) == 0
         plan.run()
         backend.sync()
-        got = read(backend, bufs, B)
+        got = read(backend, bufs, B, dims)
         for name, g, e, r in zip(("h", "qkv", "gate_up", "logits"), got, ref_eager, ref64):
             assert np.array_equal(bits(g), bits(e)), f"replay {replay}: {name} differs from the eager calls"
             assert rel_err(g.reshape(-1), r.reshape(-1)) <= 1e-4, f"replay {replay}: {name} vs oracle"
@@ -197,6 +229,18 @@ def test_decode_plan_matches_eager_and_oracle(backend, model, B):
     plan.destroy()
     for b in bufs.values():
         backend.release(b)
+
+
+@pytest.mark.parametrize("B", [1, 3, 16])
+def test_decode_plan_matches_eager_and_oracle(backend, model, B):
+    note("decode plan", "B", B)
+    check_plan(backend, model, B, SMALL)
+
+
+@pytest.mark.parametrize("B", [3, 8, 16, 19])
+def test_decode_plan_column_windows(backend, wide_model, B):
+    note("decode plan, several column windows", "B", B)
+    check_plan(backend, wide_model, B, WIDE)
 
 
 def test_decode_plan_errors(backend, model):
