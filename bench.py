@@ -565,6 +565,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only, no CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="comma list of workload groups to run: gemv,gemm,decode (default all)")
+    ap.add_argument("--batches", default="4,8,16", help="comma list of batch sizes for the batched decode-step lines")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the streaming-read ceiling and a copy kernel of known size (counter scaling)")
     args = ap.parse_args()
@@ -587,7 +588,8 @@ def main():
     others = []
     if not args.quick:
         if "decode" in groups:
-            others.append(decode_workload(eng, model, 16, max(2, args.steps // 2), max(1, args.warmup // 2)))
+            for batch in [int(b) for b in args.batches.split(",") if b]:
+                others.append(decode_workload(eng, model, batch, max(2, args.steps // 2), max(1, args.warmup // 2)))
             others.append(decode_workload(eng, model, 1, max(2, args.steps // 4), 2, plan=False))
     model.release()
     dominant = gemv_workload(eng, DOMINANT, Q4K, 28672, 4096, 1, args.steps, args.warmup, parts=[14336, 14336])
