@@ -274,10 +274,11 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             it[0].dd = gemv::ld16(rs.d, row * (uint32_t)(K / 128), so_d) |
                        (gemv::ld16(rs.d, row * (uint32_t)(K / 128) + 2u, so_d) << 16);
         }
-        // Q4_K: the wave's slice spans up to two superblocks; lane groups 0, 1 fetch the
-        // header of the first, 2, 3 that of the second (16 rows x 32 contiguous bytes in one load)
+        // Q4_K: a slice of two superblocks: lane groups 0, 1 fetch the header of the first,
+        // 2, 3 that of the second (16 rows x 32 contiguous bytes in one load); a slice of one
+        // (16 rows): every lane fetches it, and no swap is needed
         if constexpr (FMT == Q4_K) {
-            const uint32_t hs = (uint32_t)g >> 1;
+            const uint32_t hs = NBW == 8 ? 0u : (uint32_t)g >> 1;
             const bool ok = live && blkw + 8 * (int)hs < nb;
             it[0].meta = ld128(rs.sc, row * (uint32_t)(K / 16) + 16u * hs, ok ? (uint32_t)(blkw >> 3) * 16u : kOob);
         }
@@ -450,16 +451,20 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         // item (A: block sums of the hi batch rows, B: dmin * m of each row's 4 blocks), in
         // the result layout of the block products
         f32x4 corr4 = {0.f, 0.f, 0.f, 0.f};
-        // Q4_K: both superblock headers of the slice in every lane: one swap of the lane
+        // Q4_K: the slice's superblock headers in every lane: with two, one swap of the lane
         // halves per dword (hdr[0] from groups 0, 1; hdr[1] from groups 2, 3)
         uint32_t hdr[2][4] = {};
         if constexpr (FMT == Q4_K) {
             const uint32_t m4[4] = {it[0].meta.x, it[0].meta.y, it[0].meta.z, it[0].meta.w};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const auto sw = __builtin_amdgcn_permlane32_swap(m4[k], m4[k], false, false);
-                hdr[0][k] = sw[0];
-                hdr[1][k] = sw[1];
+                if constexpr (NBW == 8) {
+                    hdr[0][k] = m4[k];
+                } else {
+                    const auto sw = __builtin_amdgcn_permlane32_swap(m4[k], m4[k], false, false);
+                    hdr[0][k] = sw[0];
+                    hdr[1][k] = sw[1];
+                }
             }
         }
         // Q4_0: item i's scales live in lane group i of it[0].d; broadcast them to all groups
