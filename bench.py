@@ -54,6 +54,8 @@ LLAMA3_8B_HEAD = (Q6K, 128256, 4096)
 # GEMV, 28672 x 4096 Q4_K at batch 1. Its HBM bytes per launch were measured with rocprofv3
 # FETCH_SIZE / WRITE_SIZE counters scaled by a copy kernel of known size (see the .md beside it).
 DOMINANT = "q4_k_gemv_gate_up_fused_b1"
+# hipDeviceAttribute_t value of hipDeviceAttributeWallClockRate (kHz of the clock j4q_gemv_trace stamps)
+HIP_ATTR_WALL_CLOCK_RATE = 10017
 
 
 def log(*a):
@@ -75,6 +77,9 @@ class Hip:
             "hipEventRecord": [C.c_void_p, C.c_void_p],
             "hipEventSynchronize": [C.c_void_p],
             "hipEventElapsedTime": [C.POINTER(C.c_float), C.c_void_p, C.c_void_p],
+            "hipMemset": [C.c_void_p, C.c_int, C.c_size_t],
+            "hipMemcpy": [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int],
+            "hipDeviceGetAttribute": [C.POINTER(C.c_int), C.c_int, C.c_int],
         }.items():
             fn = getattr(self.h, name)
             fn.argtypes = args
@@ -389,6 +394,74 @@ def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n:
     }
 
 
+def timeline_workload(eng: Engine, name: str, qt: QuantType, rows: int, cols: int, parts=None, launches: int = 40):
+    """Per-wave timeline of one batch-1 GEMV launch (j4q_gemv_trace): `launches` back-to-back
+    launches over rotating weight copies, the last one traced. Reports, in us from the first
+    wave's start, when waves start, when their x image is staged, when they finish, and how
+    long x staging and each wave's items took (percentiles over the waves), by items per wave."""
+    blob_bytes = qt.byte_size_for(rows * cols)
+    copies = max(2, math.ceil(ROTATE_BYTES / blob_bytes))
+    ws = []
+    for i in range(copies):
+        if parts:
+            ps = [eng.weights(qt, r, cols, 0x71E + 97 * i + j)[0] for j, r in enumerate(parts)]
+            ws.append(eng.be.concat_rows(ps))
+            for p in ps:
+                eng.be.release(p)
+        else:
+            ws.append(eng.weights(qt, rows, cols, 0x71E + 97 * i)[0])
+    x = eng.f32(cols, 0x71F)
+    y = eng.hip.malloc(4 * rows)
+    max_waves = 16 * eng.info["compute_units"] * 8
+    words = 4 * max_waves
+    buf = eng.hip.malloc(8 * words)
+    eng.hip.ok(eng.hip.h.hipMemset(C.c_void_p(buf), 0, 8 * words), "hipMemset")
+    fn = eng.lib.j4q_quant_matvec_into
+    s = C.c_void_p(eng.stream)
+
+    def enqueue(i):
+        check(fn(ws[i % copies].handle, C.c_void_p(x), None, C.c_void_p(y), 1, s), name)
+
+    eng.time_region(enqueue, 5)
+    # every launch of the region overwrites the trace: the last one's stamps remain
+    check(eng.lib.j4q_gemv_trace(C.c_void_p(buf), words), "gemv_trace")
+    ms, _, _, _, _ = eng.time_region(enqueue, launches)
+    check(eng.lib.j4q_gemv_trace(None, 0), "gemv_trace")
+    host = (C.c_uint64 * words)()
+    eng.hip.ok(eng.hip.h.hipMemcpy(host, C.c_void_p(buf), 8 * words, 2), "hipMemcpy")
+    for w in ws:
+        eng.be.release(w)
+    for p in (x, y, buf):
+        eng.hip.free(p)
+    rec = [(host[4 * i], host[4 * i + 1], host[4 * i + 2], host[4 * i + 3] & 0xFFFFFFFF) for i in range(max_waves)]
+    rec = [r for r in rec if r[0]]
+    return name, ms / launches, rec
+
+
+def summarize_timeline(name, ms_per_launch, rec, ticks_per_us):
+    t0 = min(r[0] for r in rec)
+    start = sorted((r[0] - t0) / ticks_per_us for r in rec)
+    staged = sorted((r[1] - t0) / ticks_per_us for r in rec)
+    end = sorted((r[2] - t0) / ticks_per_us for r in rec)
+    xdur = sorted((r[1] - r[0]) / ticks_per_us for r in rec)
+    work = sorted((r[2] - r[1]) / ticks_per_us for r in rec)
+
+    def pct(v):
+        k = len(v)
+        return {f"p{q}": round(v[min(k - 1, int(q * k / 100))], 2) for q in (0, 10, 50, 90, 100)}
+
+    by_items = {}
+    for it in sorted({r[3] for r in rec}):
+        e = sorted((r[2] - t0) / ticks_per_us for r in rec if r[3] == it)
+        by_items[str(it)] = {"waves": len(e), "end_us": pct(e)}
+    out = {"workload": name, "us_per_launch": round(1e3 * ms_per_launch, 3), "waves": len(rec), "start_us": pct(start),
+           "x_staged_us": pct(staged), "x_staging_us": pct(xdur), "work_us": pct(work), "end_us": pct(end),
+           "end_by_items": by_items}
+    log(f"timeline {name}: {out['us_per_launch']} us/launch, {len(rec)} waves; start {pct(start)}; "
+        f"x staged {pct(staged)}; end {pct(end)}")
+    return out
+
+
 # Sizes of the streaming-read calibration: the algorithmic bytes of configs[0], [1], [2] (Q4_K,
 # Q6_K), the fused gate|up matrix and the output head.
 CALIBRATION_BYTES = [17858560, 25422848, 33103872, 48242688, 66060288, 430940160]
@@ -568,6 +641,9 @@ def main():
     ap.add_argument("--batches", default="4,8,16", help="comma list of batch sizes for the batched decode-step lines")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the streaming-read ceiling and a copy kernel of known size (counter scaling)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="also record the per-wave timeline of one launch of the dominant GEMV and of the step's "
+                         "smaller B = 1 GEMVs (j4q_gemv_trace)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -594,6 +670,17 @@ def main():
     model.release()
     dominant = gemv_workload(eng, DOMINANT, Q4K, 28672, 4096, 1, args.steps, args.warmup, parts=[14336, 14336])
     cal = calibrate(eng, args.steps, args.warmup) if args.calibrate else None
+    timeline = None
+    if args.timeline:
+        khz = C.c_int()
+        eng.hip.ok(eng.hip.h.hipDeviceGetAttribute(C.byref(khz), HIP_ATTR_WALL_CLOCK_RATE, 0), "hipDeviceGetAttribute")
+        tpu = khz.value / 1e3
+        timeline = [summarize_timeline(*timeline_workload(eng, *w), tpu) for w in (
+            (DOMINANT, Q4K, 28672, 4096, [14336, 14336]),
+            ("q4_k_gemv_qkv_fused_b1", Q4K, 6144, 4096, [4096, 1024, 1024]),
+            ("q4_k_gemv_o_b1", Q4K, 4096, 4096, None),
+            ("q6_k_gemv_down_b1", Q6K, 4096, 14336, None),
+        )]
     if not args.quick:
         if "gemv" in groups:
             others.append(gemv_workload(eng, "q4_0_gemv_b1", QuantType.Q4_0, 11008, 4096, 1, args.steps, args.warmup))
@@ -648,6 +735,7 @@ def main():
         "workloads": [head, dominant] + others,
         "cpu_rows": cpu_all,
         "calibration": cal,
+        "timeline": timeline,
         "host": host_description(),
         "device": eng.info,
     }

@@ -313,6 +313,12 @@ int j4q_copy(void *device_dst, const void *device_src, uint64_t nbytes, void *st
  * words): the practical HBM read ceiling of a single launch of that size, against which the
  * GEMV launches are measured. 1..4 workgroups of 512 threads per CU. */
 int j4q_stream_read(const void *device_src, uint64_t nbytes, uint32_t *sink, int32_t workgroups_per_cu, void *stream);
+/* Per-wave timeline of the batch-1 vector-ALU GEMV launches enqueued while it is set:
+ * wave w < n_words / 4 writes device_words[4 w .. 4 w + 3] = {wall clock (the device's
+ * constant-rate clock, hipDeviceAttributeWallClockRate) at entry, after x is staged, after
+ * its last item, items | (hardware CU id << 32)}; every such launch overwrites them. NULL turns
+ * it off. A decode plan records the setting at creation. */
+int j4q_gemv_trace(uint64_t *device_words, int64_t n_words);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,7 @@
 namespace j4q {
 int64_t gemv_single_pass_cols();
 void gemv_set_cus(int cus);
+void gemv_set_trace(uint64_t *words, int64_t n);
 }
 
 namespace {
@@ -936,6 +937,14 @@ int j4q_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int32_t wo
     hipDeviceProp_t p;
     HIP_TRY("hipGetDeviceProperties", hipGetDeviceProperties(&p, g_dev));
     HIP_TRY("stream_read", j4q::launch_stream_read(src, nbytes, sink, workgroups_per_cu * p.multiProcessorCount, pick_stream(stream)));
+    return J4Q_OK;
+}
+
+int j4q_gemv_trace(uint64_t *device_words, int64_t n_words) {
+    if (device_words && (n_words < 4 || !aligned(device_words, 8)))
+        return fail(J4Q_EINVAL, "gemv_trace: need at least 4 words (one wave), 8-byte aligned");
+    std::lock_guard<std::mutex> lk(g_mu);
+    j4q::gemv_set_trace(device_words, device_words ? n_words : 0);
     return J4Q_OK;
 }
 

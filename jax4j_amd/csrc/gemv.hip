@@ -4,6 +4,14 @@
 #include "gemv_mfma.h"
 
 namespace j4q {
+namespace gemv {
+TraceSink g_gemv_trace = {nullptr, 0};
+}  // namespace gemv
+
+void gemv_set_trace(uint64_t *words, int64_t n) {
+    gemv::g_gemv_trace.p = n >= 4 ? words : nullptr;
+    gemv::g_gemv_trace.waves = n >= 4 ? (int)(n / 4 < 0x7fffffff ? n / 4 : 0x7fffffff) : 0;
+}
 
 // Widest K one vector-ALU launch covers (x image in LDS); a wider K runs as column windows.
 int64_t gemv_single_pass_cols() { return gemv::kMaxWindow; }

@@ -364,11 +364,21 @@ __device__ __forceinline__ Rsrc rsrc_of(const QMat &m, int fmt) {
 // windows chained through prev (the previous window's y, read by the wave that rewrites that
 // element) with the caller's add joining only in the last window. Requires KW % 32 == 0,
 // KW / 32 <= NP, KW / 4 <= XU * WAVES * 64 and every section < 2^31 bytes.
+// Optional per-wave timeline of a launch (engine-local measurement, j4q_gemv_trace): with
+// `p` set, wave w < waves of the first batch row writes p[4 w ..] = {wall clock at entry,
+// after x is staged, after its last item, items | (hardware CU id << 32)}; null: no trace.
+struct TraceSink {
+    uint64_t *p;
+    int waves;
+};
+extern TraceSink g_gemv_trace;
+
 template <int FMT, int R, int WAVES, int D, int XU, int NP>
 __global__ void __launch_bounds__(WAVES * 64)
 gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float *add, float *y, int groups, int st0,
-            int KW) {
+            int KW, TraceSink trace) {
     extern __shared__ f32x4 lds[];
+    const uint64_t tt0 = trace.p ? wall_clock64() : 0;
     const int K = (int)m.cols, N = (int)m.rows;
     // blockIdx.y selects a batch row (each batch row streams W again; batched decode uses
     // the MFMA kernel instead).
@@ -420,6 +430,7 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
     float *s16 = reinterpret_cast<float *>(lds + 8 * NP);
     xst.store(KW, xs, s16);
     __syncthreads();
+    const uint64_t tt1 = trace.p ? wall_clock64() : 0;
 
     const float2 *s16v = reinterpret_cast<const float2 *>(s16);
     float acc[R];
@@ -465,13 +476,21 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
             load_item(i + d + D, set[d]);
         }
     }
+    if (trace.p && blockIdx.y == 0 && gw < trace.waves && lane == 0) {
+        uint64_t *t = trace.p + 4 * (int64_t)gw;
+        t[0] = tt0;
+        t[1] = tt1;
+        t[2] = wall_clock64();
+        t[3] = (uint64_t)(uint32_t)items | ((uint64_t)__smid() << 32);
+    }
 }
 
 template <int FMT, int R, int WAVES, int D, int XU, int NP>
 hipError_t launch_k(const QMat &m, const float *x, const float *prev, const float *add, float *y, int batch, int grid,
                     int groups, int st0, int kw, hipStream_t s) {
     gemv_kernel<FMT, R, WAVES, D, XU, NP><<<dim3(grid, batch), WAVES * 64, XImage<NP>::kBytes, s>>>(m, x, prev, add, y,
-                                                                                                  groups, st0, kw);
+                                                                                                  groups, st0, kw,
+                                                                                                  g_gemv_trace);
     return hipGetLastError();
 }
 
