@@ -674,18 +674,19 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
 
 // Prefill GEMM, int8 variant: Y[m, n] = sum over blocks b, in block order, of
 // fma(float(I_b[m, n]), fl(sx[m, b] * dw[n, b]), acc) with I_b the exact int32 dot of the
 // quantized activations and the Q8_0 quants of block b. Every output is folded by one lane
 // over all of K, so results are bit-identical to a sequential fp32 loop over the blocks.
 //
-// That fold is three vector-ALU operations per output and block (convert, multiply, FMA)
-// against one v_mfma_i32_32x32x32_i8 (16 ns per SIMD, measured) per 32 x 32 outputs and
-// block: measured on MI355X at M = 512, N = K = 4096, each of the three costs ~8.5 us of
-// a 42 us kernel, and the rest is the operand traffic (L2 to LDS to registers) that the
-// vector ALU does not hide. (Taking the scale products from the matrix core instead, as
-// a v_mfma_f32_32x32x2_f32 outer product, is exact but no faster: 29 ns per SIMD each.)
+// The scale products fl(sx * dw) come from the matrix core, one v_mfma_f32_32x32x1_2b_f32
+// outer product per two blocks, so the vector ALU does two operations per output and block
+// (convert, FMA) and each lane reads two scales per block pair from LDS instead of 17 per
+// block. Measured on MI355X (N = K = 4096, quantizer included), against the products on
+// the vector ALU: M = 512 45.8 us against 50.0, M = 2048 168 against 184.
 // Tile 64 x 128 per workgroup of 8 waves (two per SIMD); wave w owns the 32 x 32 outputs of
 // rows 32 (w % 2), columns 32 (w / 2), for all of K. K advances in stages of four blocks
 // (128 bytes of every row, one cache line):
@@ -799,15 +800,25 @@ gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs
         const i32x4 q = *reinterpret_cast<const i32x4 *>(&b[kXS + rb * 128 + ((ch ^ bsw) << 4)]);
         return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i32x16{}, 0, 0, 0);
     };
+    // Scale products of blocks 2 p and 2 p + 1 of the stage on the matrix core: lane
+    // (h, l32) supplies sx of row ra and dw of column rb for block 2 p + h, and
+    // v_mfma_f32_32x32x1_2b_f32 returns the two 32 x 32 outer products (block 2 p in
+    // elements 0..15, block 2 p + 1 in 16..31) in the layout of the int8 product. Each
+    // element is a0 * b0 + 0 rounded once: the fp32 product fl(sx * dw), bar the sign of a
+    // zero, which the fold below cannot see (its accumulator is never -0).
+    auto scales = [&](const uint8_t *b, int p) {
+        const float sx = reinterpret_cast<const float *>(b + kXS + kWS)[(2 * p + h) * BM + ra];
+        const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[(2 * p + h) * BN + rb];
+        return __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dw, f32x32{}, 0, 0, 0);
+    };
+    auto half = [](const f32x32 &P, int e) {
+        return e == 0 ? __builtin_shufflevector(P, P, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15)
+                      : __builtin_shufflevector(P, P, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
+    };
     // result element v: row 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32
-    auto fold = [&](const uint8_t *b, int kb, const i32x16 &I) {
-        const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[kb * BN + rb];
-        const float *sxp = reinterpret_cast<const float *>(b + kXS + kWS) + kb * BM + 32 * wm + 4 * h;
-        f32x4 sx[4];
+    auto fold = [&](const i32x16 &I, const f32x16 &p) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) sx[i] = *reinterpret_cast<const f32x4 *>(sxp + 8 * i);
-#pragma unroll
-        for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], __fmul_rn(sx[v >> 2][v & 3], dw), acc[v]);
+        for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], p[v], acc[v]);
     };
 
 #pragma unroll
@@ -830,15 +841,26 @@ gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs
             const uint8_t *b = lds + (r & 1) * kBuf;
             const int kb0 = i * SB;
             if (kb0 + SB <= nblk) {
-                // the four blocks' products first: the matrix core runs them back to back
-                // while the vector ALU folds the earlier ones
+                // the stage's products first: the matrix core runs them back to back while
+                // the vector ALU folds the earlier ones
                 i32x16 I[SB];
+                f32x32 P[SB / 2];
 #pragma unroll
-                for (int kb = 0; kb < SB; kb++) I[kb] = mfma(b, kb);
+                for (int kb = 0; kb < SB; kb++) {
+                    I[kb] = mfma(b, kb);
+                    if (kb & 1) P[kb >> 1] = scales(b, kb >> 1);
+                }
 #pragma unroll
-                for (int kb = 0; kb < SB; kb++) fold(b, kb, I[kb]);
+                for (int kb = 0; kb < SB; kb++) fold(I[kb], half(P[kb >> 1], kb & 1));
             } else {
-                for (int kb = 0; kb < SB && kb0 + kb < nblk; kb++) fold(b, kb, mfma(b, kb));
+#pragma unroll
+                for (int p = 0; p < SB / 2; p++) {
+                    if (kb0 + 2 * p >= nblk) break;
+                    const f32x32 P = scales(b, p);
+#pragma unroll
+                    for (int e = 0; e < 2; e++)
+                        if (kb0 + 2 * p + e < nblk) fold(mfma(b, 2 * p + e), half(P, e));
+                }
             }
         }
     }
@@ -972,12 +994,20 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
         const long q = *reinterpret_cast<const long *>(&b[kXS + rb * 128 + ((c ^ bsw) << 4) + half]);
         return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, q, i32x4s{0, 0, 0, 0}, 0, 0, 0);
     };
+    // Scale products of the stage's four blocks on the matrix core: lane (g, r16) supplies sx
+    // of tile row r16 and dw of column rb for block g, and v_mfma_f32_16x16x1_4b_f32 returns
+    // the four 16 x 16 outer products (block kb in elements 4 kb .. 4 kb + 3) in the layout
+    // of the int8 product, each element the fp32 product fl(sx * dw) (a0 * b0 + 0 rounded
+    // once; the sign of a zero product is lost, which the fold cannot see).
+    auto scales = [&](const uint8_t *b) {
+        const float sx = reinterpret_cast<const float *>(b + kXS + kWS)[g * BM + r16];
+        const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[g * BN + rb];
+        return __builtin_amdgcn_mfma_f32_16x16x1f32(sx, dw, f32x16{}, 0, 0, 0);
+    };
     // result element j: row 4 g + j, column lane % 16 of the wave's columns
-    auto fold = [&](const uint8_t *b, int kb, const i32x4s &I) {
-        const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[kb * BN + rb];
-        const f32x4 sx = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(b + kXS + kWS) + kb * BM + 4 * g);
+    auto fold = [&](const i32x4s &I, const f32x16 &P, int kb) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[j] = __builtin_fmaf((float)I[j], __fmul_rn(sx[j], dw), acc[j]);
+        for (int j = 0; j < 4; j++) acc[j] = __builtin_fmaf((float)I[j], P[4 * kb + j], acc[j]);
     };
 
 #pragma unroll
@@ -1005,10 +1035,14 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
                 i32x4s I[SB];
 #pragma unroll
                 for (int kb = 0; kb < SB; kb++) I[kb] = mfma(b, kb);
+                const f32x16 P = scales(b);
 #pragma unroll
-                for (int kb = 0; kb < SB; kb++) fold(b, kb, I[kb]);
+                for (int kb = 0; kb < SB; kb++) fold(I[kb], P, kb);
             } else {
-                for (int kb = 0; kb < SB && kb0 + kb < nblk; kb++) fold(b, kb, mfma(b, kb));
+                const f32x16 P = scales(b);
+#pragma unroll
+                for (int kb = 0; kb < SB; kb++)
+                    if (kb0 + kb < nblk) fold(mfma(b, kb), P, kb);
             }
         }
     }
