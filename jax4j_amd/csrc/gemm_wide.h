@@ -741,30 +741,32 @@ gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs
     // block index is a per-lane offset (a buffer load's scalar offset is wave-uniform).
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(xs, (uint64_t)M * (uint64_t)nblk * 4u);
     const __amdgpu_buffer_rsrc_t dr = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
-    const uint32_t soff = m0 + lane < M ? (uint32_t)(m0 + lane) * (uint32_t)nblk * 4u : kOob;
     const int dcol = 8 * (lane & 15), dblk = lane >> 4;
-    const uint32_t doff = ((uint32_t)dblk * (uint32_t)N + (uint32_t)(n0 + dcol)) * 2u;
+    // the other waves' scale offsets are out of range: their loads move nothing
+    const uint32_t soff = wave == 0 && m0 + lane < M ? (uint32_t)(m0 + lane) * (uint32_t)nblk * 4u : kOob;
+    const uint32_t doff = wave == 1 && n0 + dcol < N ? ((uint32_t)dblk * (uint32_t)N + (uint32_t)(n0 + dcol)) * 2u : kOob;
 
     struct Set {
         u32x4 x, w[2], s, d;  // s: sx (wave 0 only), d: dw (wave 1 only)
     };
     Set set[R];
-    // Stage i covers blocks [4 i, 4 i + 4); stages at or past ns (and bytes past K) load
-    // nothing.
+    // Stage i covers blocks [4 i, 4 i + 4). The per-lane offsets are fixed and the stage
+    // enters as the scalar offset, so the loads carry no per-stage condition (a condition
+    // there became a branch, and the wait counts that the compiler derives across it waited
+    // for the first load of the same stage). Stages at or past ns take a scalar offset of
+    // 2^30: every offset is then either past the end of its buffer (the load returns zeros)
+    // or inside it. Bytes past K in a partial last stage come from the next row (or are past
+    // the end); no MFMA reads them.
     auto load = [&](int i, Set &S_) {
+        const int kb0 = i * SB;
         const bool live = i < ns;
-        const int kb0 = i * SB, k0 = kb0 * 32;
-        S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, live && k0 + xc * 16 < K ? xoff : kOob, (uint32_t)k0, 0));
+        const uint32_t kx = live ? (uint32_t)kb0 * 32u : 0x40000000u;
+        S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff, kx, 0));
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int c = (tid + 512 * j) & 7;
-            S_.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live && k0 + c * 16 < K ? woff[j] : kOob, (uint32_t)k0, 0));
-        }
-        // issued by every wave (the other waves' offsets are out of range and move nothing),
-        // so each set member has one definition
-        const bool sok = wave == 0 && live, dok = wave == 1 && live && kb0 + dblk < nblk && n0 + dcol < N;
-        S_.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, sok ? soff : kOob, (uint32_t)kb0 * 4u, 0));
-        S_.d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, dok ? doff : kOob, (uint32_t)kb0 * (uint32_t)N * 2u, 0));
+        for (int j = 0; j < 2; j++)
+            S_.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], kx, 0));
+        S_.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, soff, live ? (uint32_t)kb0 * 4u : 0x40000000u, 0));
+        S_.d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, doff, live ? (uint32_t)kb0 * (uint32_t)N * 2u : 0x40000000u, 0));
     };
     auto store = [&](const Set &S_, int buf) {
         uint8_t *const b = lds + buf * kBuf;
@@ -944,24 +946,25 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
     const bool sthr = tid < 16, dthr = tid >= 16 && tid < 32;
     const int du = tid - 16, dcol = 8 * (du & 3), dblk = du >> 2;
     const uint32_t soff = sthr && m0 + tid < M ? (uint32_t)(m0 + tid) * (uint32_t)nblk * 4u : kOob;
-    const uint32_t doff = ((uint32_t)(dblk & 3) * (uint32_t)N + (uint32_t)(n0 + dcol)) * 2u;
+    const uint32_t doff = dthr && n0 + dcol < N ? ((uint32_t)dblk * (uint32_t)N + (uint32_t)(n0 + dcol)) * 2u : kOob;
 
     struct Set {
         u32x4 x, w[2], s, d;
     };
     Set set[R];
+    // Fixed per-lane offsets and the stage as the scalar offset, as in gemm_i8_wide: stages
+    // past the range take 2^30 (every offset then past the end of its buffer or inside
+    // it); bytes past K in the last stage are never read by an MFMA.
     auto load = [&](int i, Set &S_) {
         const bool live = i < ns;
-        const int kb0 = kbs + i * SB, k0 = kb0 * 32;
-        S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, live && k0 + xc * 16 < K ? xoff : kOob, (uint32_t)k0, 0));
+        const int kb0 = kbs + i * SB;
+        const uint32_t kx = live ? (uint32_t)kb0 * 32u : 0x40000000u;
+        S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff, kx, 0));
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int c = (tid + 128 * j) & 7;
-            S_.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live && k0 + c * 16 < K ? woff[j] : kOob, (uint32_t)k0, 0));
-        }
-        const bool dok = dthr && live && kb0 + dblk < nblk && n0 + dcol < N;
-        S_.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, live ? soff : kOob, (uint32_t)kb0 * 4u, 0));
-        S_.d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, dok ? doff : kOob, (uint32_t)kb0 * (uint32_t)N * 2u, 0));
+        for (int j = 0; j < 2; j++)
+            S_.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], kx, 0));
+        S_.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, soff, live ? (uint32_t)kb0 * 4u : 0x40000000u, 0));
+        S_.d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, doff, live ? (uint32_t)kb0 * (uint32_t)N * 2u : 0x40000000u, 0));
     };
     auto store = [&](const Set &S_, int buf) {
         uint8_t *const b = lds + buf * kBuf;
