@@ -55,17 +55,26 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 // its next item the other half, which a non-temporal load fetched again (measured: B = 16
 // decode step 2.64 -> 2.45 ms).
 constexpr int kTile = 0;
-__device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, kTile));
+// A load that is not `ok` takes the out-of-range lane offset (the scalar offset stays
+// unconditional). The lane offset passes through an empty asm: with a select on the tile's
+// liveness visible in the scalar offset, the compiler split some loads into two branches,
+// and the wait counts it then derived waited for loads issued after the ones needed.
+__device__ __forceinline__ uint32_t lane_off(uint32_t vo, bool ok) {
+    uint32_t v = ok ? vo : kOob;
+    asm("" : "+v"(v));
+    return v;
 }
-__device__ __forceinline__ u32x2 ld64(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, kTile));
+__device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, bool ok) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off(vo, ok), so, kTile));
 }
-__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, kTile);
+__device__ __forceinline__ u32x2 ld64(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, bool ok) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, lane_off(vo, ok), so, kTile));
 }
-__device__ __forceinline__ uint32_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, kTile);
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, bool ok) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, lane_off(vo, ok), so, kTile);
+}
+__device__ __forceinline__ uint32_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, bool ok) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, lane_off(vo, ok), so, kTile);
 }
 
 // On entry lane group g (lanes 16g..16g+15) holds v[0..3] = dwords 0..3 of its own unit g;
@@ -113,8 +122,7 @@ struct Fmt<Q4_0> {
     u32x4 q;
     u32x2 d;  // unused: the tile's scales are loaded once per tile (see load_tile)
     __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
-        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob;
-        q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
+        q = ld128(r.qs, row * (K / 2u) + 16u * g, (uint32_t)blk0 * 16u, live);
     }
 };
 
@@ -127,8 +135,7 @@ struct Fmt<Q4_K> {
     // tile, into item 0 (see load_tile)
     u32x4 meta;
     __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
-        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob;
-        q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
+        q = ld128(r.qs, row * (K / 2u) + 16u * g, (uint32_t)blk0 * 16u, live);
     }
 };
 
@@ -139,9 +146,8 @@ struct Fmt<Q8_0> {
     u32x4 q;
     uint32_t d;  // fp16 d of blocks 0..1
     __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
-        const uint32_t so_q = live ? (uint32_t)blk0 * 32u : kOob, so_s = live ? (uint32_t)blk0 * 2u : kOob;
-        q = ld128(r.qs, row * K + 16u * g, so_q);
-        d = ld32(r.sc, row * (K / 16u), so_s);
+        q = ld128(r.qs, row * K + 16u * g, (uint32_t)blk0 * 32u, live);
+        d = ld32(r.sc, row * (K / 16u), (uint32_t)blk0 * 2u, live);
     }
 };
 
@@ -156,10 +162,8 @@ struct Fmt<Q6_K> {
     u32x4 sca, scb;
     uint32_t dd;
     __device__ __forceinline__ void load(const Rsrc &r, uint32_t row, uint32_t K, uint32_t g, int blk0, bool live) {
-        const uint32_t so_q = live ? (uint32_t)blk0 * 16u : kOob;
-        const uint32_t so_h = live ? (uint32_t)blk0 * 8u : kOob;
-        q = ld128(r.qs, row * (K / 2u) + 16u * g, so_q);
-        h = ld64(r.qh, row * (K / 4u) + 8u * g, so_h);
+        q = ld128(r.qs, row * (K / 2u) + 16u * g, (uint32_t)blk0 * 16u, live);
+        h = ld64(r.qh, row * (K / 4u) + 8u * g, (uint32_t)blk0 * 8u, live);
     }
 };
 
@@ -272,18 +276,18 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
             it[i].load(rs, row, (uint32_t)K, (uint32_t)g, blkw + i * S, live && blkw + i * S < nb);
         if constexpr (FMT == Q4_0) {
             const bool ok = live && g < IPW && blkw + g * S < nb;
-            it[0].d = ld64(rs.sc, row * (uint32_t)(K / 16) + 8u * (uint32_t)g, ok ? (uint32_t)blkw * 2u : kOob);
+            it[0].d = ld64(rs.sc, row * (uint32_t)(K / 16) + 8u * (uint32_t)g, (uint32_t)blkw * 2u, ok);
         }
         // Q6_K: every lane fetches its row's scales of the slice (two 16-byte loads) and both
         // superblock scales: four loads per tile instead of two per item
         if constexpr (FMT == Q6_K) {
-            const uint32_t so = live ? (uint32_t)blkw * 2u : kOob;
-            it[0].sca = ld128(rs.sc, row * (uint32_t)(K / 16), so);
-            it[0].scb = ld128(rs.sc, row * (uint32_t)(K / 16) + 16u, so);
+            const uint32_t so = (uint32_t)blkw * 2u;
+            it[0].sca = ld128(rs.sc, row * (uint32_t)(K / 16), so, live);
+            it[0].scb = ld128(rs.sc, row * (uint32_t)(K / 16) + 16u, so, live);
             // two 16-bit loads: a row's d section (K / 128 bytes) is only 2-byte aligned
-            const uint32_t so_d = live ? (uint32_t)(blkw >> 3) * 2u : kOob;
-            it[0].dd = ld16(rs.d, row * (uint32_t)(K / 128), so_d) |
-                       (ld16(rs.d, row * (uint32_t)(K / 128) + 2u, so_d) << 16);
+            const uint32_t so_d = (uint32_t)(blkw >> 3) * 2u;
+            it[0].dd = ld16(rs.d, row * (uint32_t)(K / 128), so_d, live) |
+                       (ld16(rs.d, row * (uint32_t)(K / 128) + 2u, so_d, live) << 16);
         }
         // Q4_K: a slice of two superblocks: lane groups 0, 1 fetch the header of the first,
         // 2, 3 that of the second (16 rows x 32 contiguous bytes in one load); a slice of one
@@ -291,7 +295,7 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
         if constexpr (FMT == Q4_K) {
             const uint32_t hs = NBW == 8 ? 0u : (uint32_t)g >> 1;
             const bool ok = live && blkw + 8 * (int)hs < nb;
-            it[0].meta = ld128(rs.sc, row * (uint32_t)(K / 16) + 16u * hs, ok ? (uint32_t)(blkw >> 3) * 16u : kOob);
+            it[0].meta = ld128(rs.sc, row * (uint32_t)(K / 16) + 16u * hs, (uint32_t)(blkw >> 3) * 16u, ok);
         }
         const int ar = tile * 16 + rn;
         const bool aok = live && (int)threadIdx.x < 16 * BB && rb < B && ar < N;
