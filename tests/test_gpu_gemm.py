@@ -130,6 +130,42 @@ def test_gemm_int8_wide_tiles_bit_exact(backend, m, n, k):
         backend.release(h)
 
 
+# The int8 kernels take the scale products fl(sx * dw) from an fp32 outer-product MFMA,
+# a * b + 0 rounded once: bit-identical to the product except that a zero product comes out
+# +0 where the product is -0 (sx = 0 against a negative dw, or dw = -0). The fold
+# fma(float(I), p, acc) cannot tell them apart, since acc starts at +0 and never becomes -0.
+# Planted here: all-zero activation blocks (sx = 0), weight blocks with d = +0, -0 and
+# negative d, on the 16 x 32 kernel (four K ranges and one) and the 64 x 128 kernel.
+@pytest.mark.parametrize("m,n,k", [(64, 64, 256), (96, 3000, 160), (512, 136, 256)])
+def test_gemm_int8_zero_and_negative_scales_bit_exact(backend, m, n, k):
+    note("gemm int8 zero scales", m, n, k)
+    seed = 5000 + m + n + k
+    w_blob = S.quant_blocks(QuantType.Q8_0, seed, n, k)
+    nb = k // 32
+    blocks = w_blob.reshape(n * nb, 34)
+    d = blocks[:, :2].copy().view(np.uint16).reshape(-1)
+    rng = np.random.default_rng(seed)
+    pick = rng.permutation(n * nb)
+    d[pick[0::7]] = 0x0000  # +0
+    d[pick[1::7]] = 0x8000  # -0
+    d[pick[2::7]] |= 0x8000  # negative
+    blocks[:, :2] = d.view(np.uint8).reshape(-1, 2)
+    xb = S.activations_bf16(seed + 1, m * k).reshape(m, k)
+    for r in range(0, m, 3):
+        b = (r * 5) % nb
+        xb[r, 32 * b:32 * b + 32] = 0  # sx = 0
+    w = backend.upload_quantized(w_blob, QuantType.Q8_0, (n, k))
+    x = backend.upload(xb, shape=(m, k), dtype=DType.BF16)
+    y = backend.quant_matmul(w, x, "int8")
+    got = backend.download(y).reshape(m, n)
+    xq, xs = oracle.quantize_act(xb, m, k)
+    assert (xs == 0).any() and (d == 0x8000).any()
+    emu = oracle.gemm_int8_emulated(xq, xs, w_blob, m, n, k, ranges=int8_ranges(m, n, k))
+    assert np.array_equal(bits(got), bits(emu))
+    for h in (w, x, y):
+        backend.release(h)
+
+
 # M >= 512 runs the wide-tile kernel: 128 x 64 tiles while 128 x 128 ones would be fewer
 # than 256 (one stage; a half stage at the end; tails in M and N), 128 x 128 from 256 tiles.
 # The bf16 variant above M = 64 with even N loads its tiles straight into LDS when the grid
