@@ -249,6 +249,16 @@ struct Chunk;
 
 // Loads and the per-chunk scale math of each format. `so` holds the wave-uniform offsets
 // of the chunk's row and step; `j` (Q4_K) is the chunk's sub-block within its superblock.
+// A loaded register read through an empty volatile asm where it is first used: the
+// compiler otherwise hoisted the unpacking of a set's scales into the previous iteration,
+// right behind the loads that fill them, and waited there for those loads (Q6_K: an HBM
+// round trip every other item).
+template <class T>
+__device__ __forceinline__ T at_use(T v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 template <>
 struct Chunk<Q4_0> {
     u32x4 q;
@@ -260,7 +270,7 @@ struct Chunk<Q4_0> {
     __device__ __forceinline__ float apply(const XChunk &x, f32x2 sx, float acc, int) const {
         float slo = 0.f, shi = 0.f;
         q4_dot(q, x, slo, shi);
-        const float df = half_bits_to_float(d);
+        const float df = half_bits_to_float(at_use(d));
         const float t = __builtin_fmaf(shi, 0.0625f, slo);
         acc = __builtin_fmaf(-8.0f * df, sx.x + sx.y, acc);
         return __builtin_fmaf(df * kTwo24, t, acc);
@@ -279,7 +289,7 @@ struct Chunk<Q8_0> {
     __device__ __forceinline__ float apply(const XChunk &x, f32x2 sx, float acc, int) const {
         float s0 = 0.f, s1 = 0.f;
         q8_dot(qa, qb, x, s0, s1);
-        const float df = half_bits_to_float(d);
+        const float df = half_bits_to_float(at_use(d));
         acc = __builtin_fmaf(-128.0f * df, sx.x + sx.y, acc);
         return __builtin_fmaf(df * kTwo24, s0 + s1, acc);
     }
@@ -295,6 +305,7 @@ struct Chunk<Q4_K> {
     __device__ __forceinline__ float apply(const XChunk &x, f32x2 sx, float acc, int j) const {
         float slo = 0.f, shi = 0.f;
         q4_dot(q, x, slo, shi);
+        const u32x4 meta = at_use(this->meta);
         const float d = half_bits_to_float(meta.x & 0xFFFFu), dmin = half_bits_to_float(meta.x >> 16);
         const uint32_t sc = __builtin_amdgcn_ubfe(meta.y, 4 * j, 4) | (__builtin_amdgcn_ubfe(meta.w, 2 * j, 2) << 4);
         const uint32_t mn = __builtin_amdgcn_ubfe(meta.z, 4 * j, 4) | (__builtin_amdgcn_ubfe(meta.w, 16 + 2 * j, 2) << 4);
@@ -319,7 +330,8 @@ struct Chunk<Q6_K> {
     __device__ __forceinline__ float apply(const XChunk &x, f32x2 sx, float acc, int) const {
         float slo = 0.f, shi = 0.f;
         q6_dot(q, h, x, slo, shi);
-        const float df = half_bits_to_float(d);
+        const uint32_t s = at_use(this->s);
+        const float df = half_bits_to_float(at_use(d));
         const float da = df * (float)(int8_t)(s & 0xFF), db = df * (float)(int8_t)(s >> 8);
         // sum (q - 32) x stays in the fields' units (2^-24 low, 2^-20 high) and the restoring
         // power of two rides on the scale: sum (q - 32) x itself exceeds fp32 for |x| above
@@ -341,7 +353,7 @@ struct Chunk<Q2_0> {
     __device__ __forceinline__ float apply(const XChunk &x, f32x2 sx, float acc, int) const {
         float s0 = 0.f, s1 = 0.f;
         q2_dot(q, x, s0, s1);
-        const float df = half_bits_to_float(d);
+        const float df = half_bits_to_float(at_use(d));
         acc = __builtin_fmaf(-df, sx.x + sx.y, acc);
         return __builtin_fmaf(df * kTwo24, s0 + s1, acc);
     }
@@ -433,8 +445,14 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
     }
     // D register sets form a ring: set d holds items d, d + D, d + 2D, ...
     Chunk<FMT> set[D][R];
+    // one set's loads after the other, as in the loop: with the sets' loads interleaved here
+    // (q of both, then scales of both), the wait counts the compiler derives for the loop
+    // from both paths into it waited, for a set's scales, for the next set's quants too
 #pragma unroll
-    for (int d = 0; d < D; d++) load_item(d, set[d]);
+    for (int d = 0; d < D; d++) {
+        load_item(d, set[d]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     f32x4 *xs = lds;
     float *s16 = reinterpret_cast<float *>(lds + 8 * NP);
