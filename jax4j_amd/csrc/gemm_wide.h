@@ -694,8 +694,8 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 //    16-byte chunk c of row r at chunk c ^ ((r / 2) % 8) of 128-byte rows, so the 16 rows of
 //    an operand read fall on distinct banks;
 //  - sx (the activation scales, [M][K / 32]): 16 bytes of each of the 64 rows per stage,
-//    loaded by wave 0 and stored block-major in LDS, so a lane's four rows of a result
-//    group are one 16-byte read;
+//    loaded by wave 0 and stored block-major in LDS, so the 32 lanes that supply one
+//    block's sx to the scale-product MFMA read 32 consecutive floats;
 //  - dw from the block-major scale copy of the Q8_0 split layout, loaded by wave 1 and
 //    stored as fp32 in LDS.
 // Two LDS buffers and one barrier per stage; global loads run R stages ahead in a ring of
