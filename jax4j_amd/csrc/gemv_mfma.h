@@ -202,7 +202,7 @@ constexpr int round_tiles() { return BB <= 8 && WAVES <= 8 ? 4 : 2; }
 // of 8, so every slice starts on a superblock), kbn <= WAVES * NBW and B <= BB. XREG keeps
 // the wave's A operands and C inputs in registers for the whole kernel instead of
 // re-reading them from LDS per tile.
-template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS>
+template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS, bool NB = false>
 __global__ void __launch_bounds__(WAVES * 64)
 gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const float *__restrict__ add, float *y,
                  int B, int kb0, int per, int nbe, float *__restrict__ wsum) {
@@ -660,11 +660,22 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
 #pragma unroll
             for (int k = 0; k < RT; k++) {
                 const int tk = tr + k * tstep;
-                if (tk >= tiles) break;
                 const int slot = (rr * RT + k) % TS;
-                process(tset[slot], avs[slot], k);
-                load_tile(tset[slot], avs[slot], tk + TS * tstep);
-                ns = k + 1;
+                if constexpr (NB) {
+                    // every slot's loads on every path (past the last tile they load
+                    // nothing): a skip path joined into the following tiles' code makes the
+                    // compiler's merged wait counts wait for the next tile's loads
+                    if (tk < tiles) {
+                        process(tset[slot], avs[slot], k);
+                        ns = k + 1;
+                    }
+                    load_tile(tset[slot], avs[slot], tk + TS * tstep);
+                } else {
+                    if (tk >= tiles) break;
+                    process(tset[slot], avs[slot], k);
+                    load_tile(tset[slot], avs[slot], tk + TS * tstep);
+                    ns = k + 1;
+                }
             }
             finish(tr, ns);
         }
@@ -673,14 +684,14 @@ gemv_mfma_kernel(QMat m, const float *__restrict__ x, const float *prev, const f
 
 // One launch: `windows` windows of `per` blocks from kb0 (the last ends at nbe), `grid`
 // workgroups each; several windows need `part` (windows x B x rows floats).
-template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS = 2>
+template <int FMT, int BB, int WAVES, int IPW, bool XREG, int TS = 2, bool NB = false>
 hipError_t launch_k(const QMat &m, const float *x, const float *add, float *y, int B, int grid, hipStream_t s, int kb0,
                     int per, int nbe, const float *prev, int windows, float *part) {
     constexpr int NBW = IPW * Fmt<FMT>::S;
     constexpr int lds = Plan<BB, Fmt<FMT>::GROUPS, WAVES, NBW, round_tiles<BB, WAVES>()>::kBytes;
     static_assert(lds <= 160 * 1024, "LDS of one workgroup");
     if (windows > 1 && !part) return hipErrorInvalidValue;
-    gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS><<<dim3(grid, windows), WAVES * 64, lds, s>>>(
+    gemv_mfma_kernel<FMT, BB, WAVES, IPW, XREG, TS, NB><<<dim3(grid, windows), WAVES * 64, lds, s>>>(
         m, x, prev, add, y, B, kb0, per, nbe, windows > 1 ? part : nullptr);
     return hipGetLastError();
 }
