@@ -234,6 +234,37 @@ def test_gemv_batched_matches_oracle(backend, uploaded, qt, rows, cols, B):
         backend.release(h)
 
 
+# Up to 8 rows, Q4_K and Q6_K run rounds of 4 tiles, and a launch whose workgroups hold at
+# least one full round takes the tile loop without skip paths (every slot's loads on every
+# path, the compute behind the tile test). 28672 + 48 rows give 1795 tiles: 7 or 8 per
+# workgroup on a 256-CU device, the last round partial; Q6_K 4096 x 14336 runs four column
+# windows of 64 workgroups and 4 tiles each. Checked against the oracle row by row, and
+# bit-identical under a batch permutation and an exact scaling of x.
+@pytest.mark.parametrize("qt,rows,cols", [(QuantType.Q4_K, 28672 + 48, 4096), (QuantType.Q6_K, 4096, 14336)],
+                         ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [4, 8])
+def test_gemv_batched_full_rounds_match_oracle(backend, qt, rows, cols, B):
+    note("batched full rounds", qt.name, rows, cols, "B", B)
+    blob = S.quant_blocks(qt, 0x5A0 + rows, rows, cols)
+    w = backend.upload_quantized(blob, qt, (rows, cols))
+    xs = S.activations_f32(rows + 11 * B, B * cols).reshape(B, cols)
+    xb = backend.upload(xs, shape=(B, cols))
+    y = backend.quant_matvec(w, xb)
+    got = backend.download(y).reshape(B, rows)
+    for b in range(B):
+        y64 = oracle.matvec_f64(qt.id, blob, rows, cols, xs[b])
+        assert rel_err(got[b], y64) <= 4e-5, f"row {b}"
+    perm = np.roll(np.arange(B), 1)
+    xp = backend.upload(np.ascontiguousarray(xs[perm]), shape=(B, cols))
+    yp = backend.quant_matvec(w, xp)
+    assert np.array_equal(bits(backend.download(yp).reshape(B, rows)), bits(got[perm]))
+    x2 = backend.upload(2.0 * xs, shape=(B, cols))
+    y2 = backend.quant_matvec(w, x2)
+    assert np.array_equal(bits(backend.download(y2).reshape(B, rows)), bits(2.0 * got))
+    for h in (w, xb, y, xp, yp, x2, y2):
+        backend.release(h)
+
+
 # K above one 4096-column launch window: the batched kernel runs equal windows, each adding
 # the previous window's y, and the caller's add joins only in the last one (11008 = three
 # windows of 116, 116 and 112 blocks; 14336 = four of 112).
