@@ -158,15 +158,16 @@ hipError_t launch_mfma(const QMat &m, const float *x, const float *add, float *y
         int grid = g_cus * (per_cu < 8 ? per_cu : 8) / windows;
         if (grid < 1) grid = 1;
         if (grid > tiles) grid = tiles;
-        // With rounds of 4 tiles (8 waves, up to 8 rows), workgroups with at least one full
-        // round take the tile loop without skip paths: A/B on one box, decode step B = 4 1.853
-        // -> 1.818 ms, B = 8 2.110 -> 2.047 ms. With fewer tiles its loads for absent tiles
-        // cost more than it saves (Q8_0 4096 x 4096 at B = 4: 9.8 -> 10.6 us), and with
-        // rounds of 2 it lost too (Q4_0 11008 x 4096 at B = 8 12.7 -> 13.0 us, B = 16 step
-        // 2.445 -> 2.458 ms).
+        // With rounds of 4 tiles (8 waves, up to 8 rows) and at 16 rows, workgroups with at
+        // least one full round take the tile loop without skip paths: A/B on one box, decode
+        // step B = 4 1.853 -> 1.818 ms, B = 8 2.110 -> 2.047 ms, B = 16 (with the prologue's
+        // tiles loaded in order) 2.443 -> 2.399 ms. With fewer tiles its loads for absent
+        // tiles cost more than it saves (Q8_0 4096 x 4096 at B = 4: 9.8 -> 10.6 us), and for
+        // Q4_0 and Q8_0 at up to 8 rows (16 waves, rounds of 2) it lost too (Q4_0 11008 x
+        // 4096 at B = 8 12.7 -> 13.0 us).
         constexpr int RT = gmf::round_tiles<BB, W>();
         hipError_t e;
-        if constexpr (RT >= 4) {
+        if constexpr (RT >= 4 || BB > 8) {
             if ((tiles + grid - 1) / grid >= RT)
                 e = gmf::launch_k<FMT, BB, W, IPW, false, mfma_ring<FMT, BB>(), true>(
                     m, x, windows == 1 ? add : nullptr, y, b, grid, s, 0, per, nb, nullptr, windows, ws.ptr);
