@@ -433,12 +433,13 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
 
     XStage<WAVES * 64, XU, NP> xst;
     xst.load(x, KW);
-    // Windows of up to 4096 columns: every wave of the workgroup issues its x loads before
-    // any wave issues weight loads (the CU returns vector-memory data in issue order, so x
-    // loads behind another wave's weight loads wait for those HBM misses). The barrier waits
-    // for no memory. Measured in four A/B pairs: o (4096 x 4096 Q4_K) 5.41 -> 5.25 us, q|k|v
-    // 6.59 -> 6.42 us; down (K = 14336, one workgroup per CU) was 1-2 % slower with it.
-    if constexpr (NP == 128) {
+    // Windows of up to 4096 and of 8193..15360 columns: every wave of the workgroup issues its
+    // x loads before any wave issues weight loads (the CU returns vector-memory data in issue
+    // order, so x loads behind another wave's weight loads wait for those HBM misses). The
+    // barrier waits for no memory. Measured in A/B pairs on one box: o (4096 x 4096 Q4_K) 5.41
+    // -> 5.25 us, q|k|v 6.59 -> 6.42 us; down (K = 14336, one workgroup per CU) 11.62 -> 11.53
+    // us once the set loads' waits were right (before that, 1-2 % slower with it).
+    if constexpr (NP == 128 || NP == 480) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
