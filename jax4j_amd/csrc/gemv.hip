@@ -281,6 +281,11 @@ uint64_t gemv_workspace_bytes(int id, const QMat &m, int64_t batch) {
         const uint64_t r = mfma_ws_any(id, m, (int)rem);
         if (r > need) need = r;
     }
+    if (batch > 16 && (rem == 1 || rem == 2) && m.cols > gemv::kMaxWindow) {
+        // launch_gemv then runs 14 or 15 rows (within the 16-row need) and a remainder of 3
+        const uint64_t r = mfma_ws_any(id, m, 3);
+        if (r > need) need = r;
+    }
     return need;
 }
 
@@ -299,10 +304,18 @@ hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, 
         return launch_valu(id, m, x, add, y, (int)batch, s);
     }
     // batch rows in launches of up to 16 on the matrix cores (every launch streams W once for
-    // its rows); a remainder of 1 or 2 rows takes the vector-ALU kernel, which is as fast there
+    // its rows); a remainder of 1 or 2 rows takes the vector-ALU kernel, which is as fast there.
+    // Above one vector-ALU window (K > 32768) that kernel chains its windows through y, so an
+    // add that is y itself would be read after the first window rewrote it: there the last
+    // full launch gives up rows so that the remainder makes 3 and stays on the matrix cores
+    // (17 -> 14 + 3, 18 -> 15 + 3). In-place and out-of-place calls split the same way, so
+    // they agree bit for bit.
     const int64_t cap = !alias || ws_ok || single_window<16>(m) ? 16 : 8;
+    const int64_t rem = batch % cap;
+    const bool wide = m.cols > gemv::kMaxWindow && batch > cap && (rem == 1 || rem == 2);
     for (int64_t b0 = 0; b0 < batch;) {
-        const int64_t nb = batch - b0 < cap ? batch - b0 : cap;
+        int64_t nb = batch - b0 < cap ? batch - b0 : cap;
+        if (wide && batch - b0 == cap + rem) nb = cap + rem - 3;
         const float *xb = x + b0 * m.cols;
         const float *ab = add ? add + b0 * m.rows : nullptr;
         float *yb = y + b0 * m.rows;

@@ -16,6 +16,10 @@ Parity status of each function (what pins it; see tests/test_oracle.py):
   the published block layouts.
 - ref_quantize_act, GEMM references: pinned by closed-form cases (constant blocks, zero
   blocks, exact powers of two) and by exact integer arithmetic checks in numpy.
+- ref_matmul_f64: each row equals ref_matvec_f64 of its batch row bit for bit, and the
+  whole product equals a numpy fp64 product of the decoded matrix within 1e-12.
+- ref_gemm_f64 / ref_gemm_bf16w_f64 (any format): equal the Q8_0 entry points bit for bit
+  on Q8_0, and a numpy fp64 product of the decoded (or bf16-rounded) weights within 1e-12.
 """
 from __future__ import annotations
 
@@ -58,6 +62,8 @@ def load():
             "ref_gemm_q8_int8_emulated": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
             "ref_gemm_q8_int8_emulated_ranges": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp],
             "ref_gemm_q8_f64": [_vp, _vp, _i64, _i64, _i64, _vp],
+            "ref_gemm_f64": [C.c_int, _vp, _vp, _i64, _i64, _i64, _vp],
+            "ref_gemm_bf16w_f64": [C.c_int, _vp, _vp, _i64, _i64, _i64, _vp],
             "ref_gemm_q8_bf16w_f64": [_vp, _vp, _i64, _i64, _i64, _vp],
         }
         res = {"ref_half_to_float": C.c_float, "ref_half_to_float_array": None, "ref_f32_to_bf16": C.c_uint16, "ref_bf16_to_f32": C.c_float}
@@ -153,8 +159,18 @@ def gemm_int8_emulated(xq, xs, w_blob, m, n, k, ranges: int = 1, stage_blocks: i
     return y
 
 
-def gemm_f64(x_bf16, w_blob, m, n, k, bf16_weights: bool = False) -> np.ndarray:
+def gemm_f64(x_bf16, w_blob, m, n, k, bf16_weights: bool = False, qtype: int = Q8_0) -> np.ndarray:
+    """Y [m, n] = X_bf16 [m, k] . W^T in double for W of type `qtype` [n, k]: the exactly
+    decoded weights, or with bf16_weights each fp32 weight rounded to bf16 first."""
+    y = np.empty((m, n), dtype=np.float64)
+    fn = load().ref_gemm_bf16w_f64 if bf16_weights else load().ref_gemm_f64
+    _ok(fn(qtype, _p(np.ascontiguousarray(x_bf16, dtype=np.uint16)), _p(w_blob), m, n, k, _p(y)), "gemm_f64")
+    return y
+
+
+def gemm_q8_f64(x_bf16, w_blob, m, n, k, bf16_weights: bool = False) -> np.ndarray:
+    """The Q8_0 entry points of the same two references."""
     y = np.empty((m, n), dtype=np.float64)
     fn = load().ref_gemm_q8_bf16w_f64 if bf16_weights else load().ref_gemm_q8_f64
-    _ok(fn(_p(np.ascontiguousarray(x_bf16, dtype=np.uint16)), _p(w_blob), m, n, k, _p(y)), "gemm_f64")
+    _ok(fn(_p(np.ascontiguousarray(x_bf16, dtype=np.uint16)), _p(w_blob), m, n, k, _p(y)), "gemm_q8_f64")
     return y

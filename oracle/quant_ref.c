@@ -384,9 +384,10 @@ int ref_gemm_q8_int8_emulated(const int8_t *xq, const float *xs, const uint8_t *
     return ref_gemm_q8_int8_emulated_ranges(xq, xs, w_blob, m, n, k, 1, 1, y);
 }
 
-static int gemm_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k, double *y,
-                    int round_w_to_bf16) {
-    if (m <= 0 || n <= 0 || k <= 0 || k % 32 != 0) return -1;
+static int gemm_f64(int type_id, const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k,
+                    double *y, int round_w_to_bf16) {
+    int be, bb;
+    if (ref_block_geometry(type_id, &be, &bb) != 0 || m <= 0 || !valid_dims(n, k, be)) return -1;
     float *w = (float *)malloc((size_t)k * sizeof(float));
     double *xd = (double *)malloc((size_t)(m * k) * sizeof(double));
     if (!w || !xd) {
@@ -395,9 +396,9 @@ static int gemm_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, in
         return -1;
     }
     for (int64_t t = 0; t < m * k; t++) xd[t] = (double)ref_bf16_to_f32(x_bf16[t]);
-    const int64_t rb = k / 32 * 34;
+    const int64_t rb = row_bytes_of(type_id, k);
     for (int64_t j = 0; j < n; j++) {
-        ref_dequant_row(REF_Q8_0, w_blob + j * rb, k, w);
+        ref_dequant_row(type_id, w_blob + j * rb, k, w);
         if (round_w_to_bf16)
             for (int64_t t = 0; t < k; t++) w[t] = ref_bf16_to_f32(ref_f32_to_bf16(w[t]));
         for (int64_t i = 0; i < m; i++) {
@@ -412,11 +413,21 @@ static int gemm_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, in
     return 0;
 }
 
+int ref_gemm_f64(int type_id, const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k,
+                 double *y) {
+    return gemm_f64(type_id, x_bf16, w_blob, m, n, k, y, 0);
+}
+
+int ref_gemm_bf16w_f64(int type_id, const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k,
+                       double *y) {
+    return gemm_f64(type_id, x_bf16, w_blob, m, n, k, y, 1);
+}
+
 int ref_gemm_q8_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k, double *y) {
-    return gemm_f64(x_bf16, w_blob, m, n, k, y, 0);
+    return gemm_f64(REF_Q8_0, x_bf16, w_blob, m, n, k, y, 0);
 }
 
 int ref_gemm_q8_bf16w_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k,
                           double *y) {
-    return gemm_f64(x_bf16, w_blob, m, n, k, y, 1);
+    return gemm_f64(REF_Q8_0, x_bf16, w_blob, m, n, k, y, 1);
 }

@@ -52,11 +52,11 @@ int ref_dequant_row(int type_id, const uint8_t *row_blocks, int64_t cols, float 
 int ref_matvec(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, const float *x, float *y);
 /* Same product accumulated in double: the brute-force tolerance reference. */
 int ref_matvec_f64(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, const float *x, double *y);
-/* Full-matrix dequantization, rows x cols fp32. */
 /* ref_matvec_f64 over a batch: x [batch][cols] -> y [batch][rows]; row b equals
  * ref_matvec_f64 of x[b] bit for bit (one decode of each weight row). */
 int ref_matmul_f64(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, const float *x, int64_t batch,
                    double *y);
+/* Full-matrix dequantization, rows x cols fp32. */
 int ref_dequant_matrix(int type_id, const uint8_t *blob, int64_t rows, int64_t cols, float *out);
 
 /* bf16 helpers: round-to-nearest-even fp32 -> bf16, and bf16 -> fp32. */
@@ -79,9 +79,17 @@ int ref_gemm_q8_int8_emulated(const int8_t *xq, const float *xs, const uint8_t *
  * above). The GPU's small-M int8 kernel uses four ranges of four-block stages. */
 int ref_gemm_q8_int8_emulated_ranges(const int8_t *xq, const float *xs, const uint8_t *w_blob, int64_t m,
                                      int64_t n, int64_t k, int64_t nranges, int64_t stage_blocks, float *y);
-/* Exact reference for both GEMM variants: Y = X_bf16 . dequant(W)^T in double. */
+/* Exact reference for both GEMM variants: Y = X_bf16 . dequant(W)^T in double, W of any
+ * supported type [n, k] (semantics: quantMatvec per row of X, cpu/CpuBackend.java:708-725,
+ * over the exactly decoded weights of ref_dequant_row). */
+int ref_gemm_f64(int type_id, const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k,
+                 double *y);
+/* bf16 variant emulation: Y = X_bf16 . bf16(dequant(W))^T in double (every fp32 weight of
+ * ref_dequant_row rounded to the nearest-even bf16 first). */
+int ref_gemm_bf16w_f64(int type_id, const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k,
+                       double *y);
+/* The two above for Q8_0 weights. */
 int ref_gemm_q8_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k, double *y);
-/* bf16 variant emulation: Y = X_bf16 . bf16(dequant(W))^T in double. */
 int ref_gemm_q8_bf16w_f64(const uint16_t *x_bf16, const uint8_t *w_blob, int64_t m, int64_t n, int64_t k,
                           double *y);
 

@@ -283,3 +283,58 @@ def _round_bf16(f: np.ndarray) -> np.ndarray:
     u = np.ascontiguousarray(f, dtype=np.float32).view(np.uint32).astype(np.uint64)
     u = u + 0x7FFF + ((u >> 16) & 1)
     return (u >> 16).astype(np.uint16)
+
+
+# ---- batched and GEMM references ---------------------------------------------------------
+
+@pytest.mark.parametrize("qt", FORMATS, ids=lambda q: q.name)
+def test_matmul_f64_rows_equal_matvec_f64_and_numpy(qt):
+    """ref_matmul_f64 (the fp64 reference of every batched GEMV check) is quantMatvec per row
+    of x (CpuBackend.java:708-725): row b equals ref_matvec_f64 of x[b] bit for bit, and the
+    whole product equals numpy's fp64 product of the independently decoded matrix."""
+    rows, batch = 37, 5  # odd rows and batch
+    cols = 2 * qt.block_elements if qt.block_elements > 32 else 96
+    blob = S.quant_blocks(qt, 31, rows, cols)
+    xs = S.activations_f32(32, batch * cols).reshape(batch, cols)
+    got = oracle.matmul_f64(qt.id, blob, rows, cols, xs)
+    assert got.shape == (batch, rows)
+    for b in range(batch):
+        row = oracle.matvec_f64(qt.id, blob, rows, cols, xs[b])
+        assert np.array_equal(got[b].view(np.uint64), row.view(np.uint64)), b
+    want = xs.astype(np.float64) @ np_dequant(qt, blob, rows, cols).astype(np.float64).T
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    # a mistake a batched loop can make: rows of x swapped between outputs
+    assert not np.allclose(got[::-1], want, rtol=1e-6)
+
+
+@pytest.mark.parametrize("qt", [QuantType.Q4_0, QuantType.Q4_K, QuantType.Q6_K, QuantType.Q8_0], ids=lambda q: q.name)
+def test_gemm_references_any_format_against_numpy(qt):
+    """ref_gemm_f64 / ref_gemm_bf16w_f64 for every format of the prefill GEMM: numpy's fp64
+    product of the independently decoded weights (and of those weights rounded to bf16,
+    round-to-nearest-even, by a separate numpy rounding), within 1e-12; on Q8_0 they equal the
+    Q8_0 entry points bit for bit."""
+    m, n = 3, 11
+    k = 512
+    w_blob = S.quant_blocks(qt, 41, n, k)
+    xb = S.activations_bf16(42, m * k).reshape(m, k)
+    xf = (xb.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    wdq = np_dequant(qt, w_blob, n, k)
+    y64 = oracle.gemm_f64(xb, w_blob, m, n, k, qtype=qt.id)
+    want = xf @ wdq.astype(np.float64).T
+    assert np.allclose(y64, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    wbf = (_round_bf16(wdq).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    ybf = oracle.gemm_f64(xb, w_blob, m, n, k, bf16_weights=True, qtype=qt.id)
+    wantbf = xf @ wbf.T
+    assert np.allclose(ybf, wantbf, rtol=1e-12, atol=1e-12 * np.abs(wantbf).max())
+    # the bf16 rounding of the weights is visible at this size (the two are not the same check)
+    assert not np.allclose(ybf, y64, rtol=1e-9, atol=0)
+    if qt == QuantType.Q8_0:
+        assert np.array_equal(y64.view(np.uint64), oracle.gemm_q8_f64(xb, w_blob, m, n, k).view(np.uint64))
+        assert np.array_equal(ybf.view(np.uint64), oracle.gemm_q8_f64(xb, w_blob, m, n, k, True).view(np.uint64))
+
+
+def test_gemm_reference_rejects_misaligned_k():
+    blob = S.quant_blocks(QuantType.Q4_K, 1, 2, 256)
+    xb = S.activations_bf16(2, 2 * 288)
+    with pytest.raises(ValueError):
+        oracle.gemm_f64(xb, blob, 2, 2, 288, qtype=QuantType.Q4_K.id)
