@@ -130,7 +130,10 @@ int j4q_download_f32(j4q_buffer buffer, float *out, int64_t count);
 /* Raw copy of any non-quantized buffer (int8 / bf16 / f32), syncing first. */
 int j4q_download_bytes(j4q_buffer buffer, void *out, uint64_t nbytes);
 int j4q_buffer_info(j4q_buffer buffer, j4q_buffer_desc *out);
-/* ComputeBackend.release (spi/ComputeBackend.java:280). Releasing 0 is a no-op. */
+/* ComputeBackend.release (spi/ComputeBackend.java:280). Releasing 0 is a no-op. A matrix
+ * that a live decode plan reads (see j4q_decode_plan_create) is refused with J4Q_EINVAL and
+ * stays valid, so memory a queued replay reads is never freed (the reference's frees never
+ * race queued work either: rocm/HipBuffer.java:33-61, rocm/HipRuntime.java:246-262). */
 int j4q_release(j4q_buffer buffer);
 /* Live buffer handles and the device bytes they hold (engine-local accounting, the
  * counterpart of the reference's Cleaner-tracked HipBuffer frees, rocm/HipBuffer.java:31-81):
@@ -166,8 +169,9 @@ int j4q_quant_matmul(j4q_buffer weights, j4q_buffer x, int variant, j4q_buffer *
 
 /* ---- stream-ordered entry points on caller memory (no sync) ----------------------------- */
 
-/* quantMatvec / quantMatvecAdd into caller device memory: x_dev [batch, cols] and y_dev
- * [batch, rows] fp32 (16-byte aligned); add_dev NULL or [batch, rows]. add_dev may be y_dev
+/* quantMatvec / quantMatvecAdd into caller device memory: x_dev [batch, cols] fp32 (16-byte
+ * aligned) and y_dev [batch, rows] fp32 (4-byte aligned); add_dev NULL or [batch, rows]
+ * (4-byte aligned). add_dev may be y_dev
  * itself (a residual updated in place) for cols <= 32768, or at batch >= 3 on Q4_0, Q8_0,
  * Q4_K and Q6_K; other adds overlapping y return J4Q_EUNSUPPORTED (column windows chained
  * one after another would read it after rewriting y). A batched call over several column
@@ -205,8 +209,11 @@ int j4q_quant_matmul_noalloc(j4q_buffer weights, const uint16_t *x_dev, int64_t 
  * gate|up run as one launch each when their parts share a quant type (the plan holds
  * row-concatenated copies, see j4q_concat_rows); otherwise as one launch per run of equal
  * types, with outputs in the same [batch][q|k|v] layout. Every layer must have the same
- * shapes; quant types may differ. The matrices must stay alive until the plan is
- * destroyed. The io pointers are bound at creation (the graph records them). */
+ * shapes; quant types may differ. The plan pins every matrix whose memory its graph reads
+ * (o, down, the head, and any q/k/v or gate/up part not concatenated into a plan-owned
+ * copy): j4q_release of one returns J4Q_EINVAL until j4q_decode_plan_destroy. The io
+ * pointers are caller memory bound at creation (the graph records them) and must outlive
+ * the plan. The GEMV trace (j4q_gemv_trace) is off inside a plan's graph. */
 typedef uint64_t j4q_plan; /* 0 is never a valid handle */
 
 typedef struct j4q_decode_layer {
@@ -317,7 +324,7 @@ int j4q_stream_read(const void *device_src, uint64_t nbytes, uint32_t *sink, int
  * wave w < n_words / 4 writes device_words[4 w .. 4 w + 3] = {wall clock (the device's
  * constant-rate clock, hipDeviceAttributeWallClockRate) at entry, after x is staged, after
  * its last item, items | (hardware CU id << 32)}; every such launch overwrites them. NULL turns
- * it off. A decode plan records the setting at creation. */
+ * it off. Decode plans capture their graphs with the trace off. */
 int j4q_gemv_trace(uint64_t *device_words, int64_t n_words);
 
 #ifdef __cplusplus

@@ -31,6 +31,10 @@ struct Buf {
     uint64_t bytes = 0;
     uint32_t gen = 0;
     bool live = false;
+    // decode plans whose captured graph reads this buffer's memory; while any lives the
+    // buffer cannot be released (last_plan names one of them in the error)
+    int32_t pins = 0;
+    uint64_t last_plan = 0;
 };
 
 // Workspace of j4q_quant_matmul_noalloc (the one entry point that allocates nothing): the
@@ -393,6 +397,19 @@ int quant_locked(j4q_buffer h, const char *op, QuantRef *out) {
     return J4Q_OK;
 }
 
+int pin_locked(j4q_buffer h, uint64_t plan) {
+    Buf *b = lookup(h);
+    if (!b) return fail(J4Q_EHANDLE, "decode plan: buffer 0x%llx was released", (unsigned long long)h);
+    b->pins++;
+    b->last_plan = plan;
+    return J4Q_OK;
+}
+
+void unpin_locked(j4q_buffer h) {
+    Buf *b = lookup(h);
+    if (b && b->pins > 0) b->pins--;
+}
+
 int concat_locked(const j4q_buffer *parts, int count, void **dev_out, QuantRef *out) {
     if (count < 1 || count > 64) return fail(J4Q_EINVAL, "concat_rows: count %d out of range [1, 64]", count);
     int rc;
@@ -658,6 +675,10 @@ int j4q_release(j4q_buffer h) {
     Buf *b;
     int rc;
     if ((rc = get_buf(h, 0, "release", &b))) return rc;
+    if (b->pins > 0)
+        return fail(J4Q_EINVAL,
+                    "release: buffer 0x%llx is read by %d live decode plan(s), e.g. 0x%llx; destroy the plan first",
+                    (unsigned long long)h, (int)b->pins, (unsigned long long)b->last_plan);
     if (b->dev) {
         if ((rc = ensure_ready())) return rc;
         // hipFree waits for work that may still read the buffer.

@@ -32,6 +32,10 @@ struct QuantRef {
 };
 // With the lock held: the quantized buffer behind `h`, or a J4Q_EHANDLE error naming `op`.
 int quant_locked(j4q_buffer h, const char *op, QuantRef *out);
+// With the lock held: records that live decode plan `plan` reads the memory of buffer `h`
+// (j4q_release refuses it until unpinned), and undoes one such record.
+int pin_locked(j4q_buffer h, uint64_t plan);
+void unpin_locked(j4q_buffer h);
 // With the lock held: a new device allocation holding the rows of `parts` in order (same
 // type and column count), in the split layout; the caller owns *dev (hipFree). Synchronises.
 int concat_locked(const j4q_buffer *parts, int count, void **dev, QuantRef *out);

@@ -13,6 +13,11 @@ void gemv_set_trace(uint64_t *words, int64_t n) {
     gemv::g_gemv_trace.waves = n >= 4 ? (int)(n / 4 < 0x7fffffff ? n / 4 : 0x7fffffff) : 0;
 }
 
+int64_t gemv_get_trace(uint64_t **words) {
+    *words = gemv::g_gemv_trace.p;
+    return gemv::g_gemv_trace.p ? 4 * (int64_t)gemv::g_gemv_trace.waves : 0;
+}
+
 // Widest K one vector-ALU launch covers (x image in LDS); a wider K runs as column windows.
 int64_t gemv_single_pass_cols() { return gemv::kMaxWindow; }
 

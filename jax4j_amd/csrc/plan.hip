@@ -27,6 +27,9 @@
 #include "engine.h"
 
 namespace j4q {
+void gemv_set_trace(uint64_t *words, int64_t n);
+int64_t gemv_get_trace(uint64_t **words);
+
 namespace {
 
 // dst[b * dst_pitch + c] = src[b * cols + c] for b < batch, c < cols (floats).
@@ -58,6 +61,11 @@ struct Plan {
     Workspace ws;  // partial sums of batched GEMVs over several column windows (plan-owned)
     std::vector<Op> ops;
     std::vector<void *> owned;
+    // caller buffers whose memory the graph reads (o, down, the head, and group parts that were
+    // not concatenated into plan-owned copies): pinned while the plan lives, so j4q_release
+    // cannot free memory a replay still reads
+    std::vector<j4q_buffer> reads;
+    bool pinned = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     uint32_t gen = 0;
@@ -84,6 +92,8 @@ hipError_t enqueue(const Plan &p, hipStream_t s) {
 }
 
 void free_plan(Plan &p) {
+    if (p.pinned)
+        for (j4q_buffer h : p.reads) abi::unpin_locked(h);
     if (p.exec) (void)hipGraphExecDestroy(p.exec);
     if (p.graph) (void)hipGraphDestroy(p.graph);
     for (void *d : p.owned) (void)hipFree(d);
@@ -125,6 +135,7 @@ int build_group(Plan &p, const j4q_buffer *parts, int count, const char *what, c
             p.desc.plan_bytes += split_layout(run.qtype, run.rows, run.cols).total;
         } else {
             run.gguf_bytes = refs[(size_t)i].gguf_bytes;
+            p.reads.push_back(parts[i]);
         }
         Op g{};
         g.gemv = true;
@@ -170,6 +181,7 @@ int one_gemv(Plan &p, j4q_buffer w, const char *what, const float *x, const floa
     g.add = add;
     g.y = y;
     p.ops.push_back(g);
+    p.reads.push_back(w);
     p.desc.gemvs_per_step++;
     p.desc.weight_bytes += r.gguf_bytes;
     return J4Q_OK;
@@ -284,7 +296,12 @@ int j4q_decode_plan_create(const j4q_decode_layer *layers, int32_t n_layers, j4q
         return rc;
     }
     // Capture one step on a private stream (thread-local mode: other threads' HIP calls are
-    // unaffected) and instantiate it; replays then cost one graph launch.
+    // unaffected) and instantiate it; replays then cost one graph launch. The GEMV trace is
+    // off while capturing: a graph that recorded the trace buffer would keep writing it after
+    // the caller turned the trace off and freed it.
+    uint64_t *trace_words = nullptr;
+    const int64_t trace_n = gemv_get_trace(&trace_words);
+    gemv_set_trace(nullptr, 0);
     hipStream_t cs = nullptr;
     e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
@@ -293,6 +310,7 @@ int j4q_decode_plan_create(const j4q_decode_layer *layers, int32_t n_layers, j4q
         e = hipStreamEndCapture(cs, &p.graph);
         if (le != hipSuccess) e = le;
     }
+    gemv_set_trace(trace_words, trace_n);
     if (e == hipSuccess) e = hipGraphInstantiate(&p.exec, p.graph, nullptr, nullptr, 0);
     if (cs) (void)hipStreamDestroy(cs);
     if (e != hipSuccess) {
@@ -305,8 +323,12 @@ int j4q_decode_plan_create(const j4q_decode_layer *layers, int32_t n_layers, j4q
     if (slot == g_plans.size()) g_plans.emplace_back();
     p.gen = g_plans[slot].gen + 1;
     p.live = true;
+    const j4q_plan handle = ((uint64_t)p.gen << 32) | (uint64_t)(slot + 1);
+    // every handle was looked up under this same lock hold, so pinning cannot fail
+    for (j4q_buffer h : p.reads) (void)abi::pin_locked(h, handle);
+    p.pinned = true;
     g_plans[slot] = std::move(p);
-    *out = ((uint64_t)g_plans[slot].gen << 32) | (uint64_t)(slot + 1);
+    *out = handle;
     return J4Q_OK;
 }
 

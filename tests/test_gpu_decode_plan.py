@@ -264,3 +264,51 @@ def test_decode_plan_errors(backend, model):
         stale.run()
     for b in bufs.values():
         backend.release(b)
+
+
+def test_decode_plan_pins_the_matrices_it_reads(backend):
+    """A plan's graph reads o, down, the head and every q/k/v or gate/up part it did not copy
+    into a fused plan-owned matrix: releasing one of those while the plan lives is refused
+    (the memory of a queued replay is never freed), the refused buffer stays valid, replays
+    still equal the eager calls, and after j4q_decode_plan_destroy they release normally.
+    Parts that were concatenated into plan-owned copies are not read by the graph and may be
+    released at once. A GEMV trace set while the plan is created is not recorded in its
+    graph: a replay after the trace was turned off writes nothing into the trace buffer."""
+    note("decode plan pins")
+    m = build_model(backend, SMALL, 0xD2C)
+    layers, blobs, head, hblob = m
+    B = 1
+    h0, xo, xd, bufs = make_io(backend, B)
+    io = {k: ptr(backend, bufs[k]) for k in ("h", "x_o", "x_down", "qkv", "gate_up", "logits")}
+    lib = N.load()
+    sentinel = np.full(4 * 4096, 0x7FC00001, np.uint32).view(np.float32)  # a NaN pattern
+    tr = backend.upload(sentinel)
+    assert lib.j4q_gemv_trace(C.c_void_p(ptr(backend, tr)), sentinel.size // 2) == 0
+    try:
+        plan = backend.decode_plan(layers, head, B, io)
+    finally:
+        assert lib.j4q_gemv_trace(None, 0) == 0
+    read_by_graph = [layers[0]["o"], layers[0]["down"], layers[1]["v"], layers[1]["o"], layers[1]["gate"],
+                     layers[1]["up"], layers[1]["down"], head]
+    for w in read_by_graph:
+        with pytest.raises(IllegalArgumentException, match="live decode plan"):
+            backend.release(w)
+        assert w.handle != 0
+    # layer 0's q, k, v (one type) and gate, up (one type) run from plan-owned concatenations
+    fused_parts = [layers[0][n] for n in ("q", "k", "v", "gate", "up")] + [layers[1][n] for n in ("q", "k")]
+    ref_eager = eager(backend, layers, head, h0, xo, xd)
+    for w in fused_parts:
+        backend.release(w)
+    for replay in range(2):
+        assert lib.j4q_copy(C.c_void_p(io["h"]), C.c_void_p(ptr(backend, bufs["h0"])), B * SMALL.D * 4, None) == 0
+        plan.run()
+        backend.sync()
+        got = read(backend, bufs, B)
+        for name, g, e in zip(("h", "qkv", "gate_up", "logits"), got, ref_eager):
+            assert np.array_equal(bits(g), bits(e)), f"replay {replay}: {name} differs from the eager calls"
+    assert np.array_equal(backend.download(tr).view(np.uint32), sentinel.view(np.uint32))
+    plan.destroy()
+    for w in read_by_graph:
+        backend.release(w)
+    for b in list(bufs.values()) + [tr]:
+        backend.release(b)

@@ -215,23 +215,28 @@ def test_gemm_bf16_lds_kernel_matches_register_staged(backend, m, n, k):
         backend.release(h)
 
 
-def test_gemm_full_size_rows_and_variants_agree(backend):
-    """configs[3] at full size (M=512, N=K=4096): sampled rows against the oracle, and the
-    two variants against each other."""
-    m, n, k = 512, 4096, 4096
+@pytest.mark.parametrize("m", [32, 128, 512, 2048])
+def test_gemm_full_size_rows_and_variants_agree(backend, m):
+    """configs[3] at full size (N = K = 4096, every M of the sweep): sampled rows (first and
+    last rows of the first, a middle and the last M tile) against the oracle, the int8 variant
+    bit for bit against the emulation with the dispatch's K ranges, the bf16 variant within
+    the accumulation-order bound of the bf16-weight product, and the two variants against each
+    other over the whole output."""
+    n, k = 4096, 4096
     note("gemm full", m, n, k)
-    w_blob, xb, w, x = upload_case(backend, m, n, k, 0x5EED8)
+    w_blob, xb, w, x = upload_case(backend, m, n, k, 0x5EED8 + m)
     yi = backend.quant_matmul(w, x, "int8")
     yb = backend.quant_matmul(w, x, "bf16")
     gi = backend.download(yi).reshape(m, n)
     gb = backend.download(yb).reshape(m, n)
-    rows = [0, 1, 255, 510, 511]
+    rows = sorted({0, 1, 15, 16, m // 2 - 1, m // 2, m - 17, m - 2, m - 1})
     sub = np.ascontiguousarray(xb[rows])
     y64 = oracle.gemm_f64(sub, w_blob, len(rows), n, k)
     assert rel_err(gi[rows], y64) <= TOL_BF16X
     assert rel_err(gb[rows], y64) <= TOL_BF16X
     xq, xs = oracle.quantize_act(sub, len(rows), k)
-    assert np.array_equal(bits(gi[rows]), bits(oracle.gemm_int8_emulated(xq, xs, w_blob, len(rows), n, k)))
+    emu = oracle.gemm_int8_emulated(xq, xs, w_blob, len(rows), n, k, ranges=int8_ranges(m, n, k))
+    assert np.array_equal(bits(gi[rows]), bits(emu))
     assert rel_err(gb[rows], oracle.gemm_f64(sub, w_blob, len(rows), n, k, bf16_weights=True)) <= TOL_ACCUM
     assert rel_err(gi, gb.astype(np.float64)) <= 2 * TOL_BF16X
     for h in (w, x, yi, yb):

@@ -544,3 +544,33 @@ def test_add_partly_overlapping_y_is_rejected(backend, uploaded):
             backend.quant_matvec_into(w, backend.buffer_desc(x).device_ptr, rp + 16, rp, B)
     backend.release(x)
     backend.release(res)
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(QuantType.Q4_0, 40, 40960), (QuantType.Q6_K, 40, 40960),
+                                          (QuantType.Q4_K, 24, 53248)], ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [17, 18, 33, 34])
+def test_batched_in_place_add_above_one_window(backend, uploaded, qt, rows, cols, B):
+    """A residual updated in place (add = y) at more than 16 batch rows over K > 32768: the
+    rows past the last full 16 stay on the matrix cores (a 1-2 row remainder on the
+    vector-ALU kernel would chain its column windows through y and read the add after the
+    first window rewrote it). Bit for bit equal to the out-of-place quantMatvecAdd, which
+    splits the batch the same way, and within the batched bound of the oracle."""
+    note("in place above one window", qt.name, rows, cols, "B", B)
+    blob, w = uploaded(qt, rows, cols)
+    xs = S.activations_f32(cols + 3 * B, B * cols).reshape(B, cols)
+    add = S.activations_f32(cols + 5 * B, B * rows).reshape(B, rows)
+    xb = backend.upload(xs, shape=(B, cols))
+    ab = backend.upload(add, shape=(B, rows))
+    ya = backend.quant_matvec_add(w, xb, ab)
+    want = backend.download(ya).reshape(B, rows)
+    res = backend.upload(add, shape=(B, rows))
+    rp = backend.buffer_desc(res).device_ptr
+    backend.quant_matvec_into(w, backend.buffer_desc(xb).device_ptr, rp, rp, B)
+    backend.sync()
+    got = backend.download(res).reshape(B, rows)
+    assert np.array_equal(bits(got), bits(want))
+    ref = oracle.matmul_f64(qt.id, blob, rows, cols, xs) + add.astype(np.float64)
+    for b in range(B):
+        assert rel_err(got[b], ref[b]) <= 1e-4, f"row {b}"
+    for h in (xb, ab, ya, res):
+        backend.release(h)
