@@ -162,9 +162,11 @@ int j4q_quant_dequantize(j4q_buffer weights, j4q_buffer *y);
 /* bf16 X [M, K] -> int8 per 32-element block with an fp32 scale per block:
  * s = amax/127, q = clamp(roundf(x * (1/s)), -127, 127) (ggml quantize_row_q8_0, fp32 scale). */
 int j4q_quantize_act(j4q_buffer x_bf16, j4q_buffer *xq_i8, j4q_buffer *scales_f32);
-/* Y F32 [M, N] = X [M, K] . W^T for a Q8_0 W [N, K]. X is bf16 (or F32, rounded to bf16
- * first). J4Q_GEMM_INT8 quantizes X per 32 and runs int8 MFMA; J4Q_GEMM_BF16 runs bf16
- * MFMA on W dequantized into LDS. */
+/* Y F32 [M, N] = X [M, K] . W^T for a quantized W [N, K] (QuantizedOps.quantMatvec applied
+ * to every row of X, QuantizedOps.java:27; CpuBackend.java:708-725). X is a bf16 buffer
+ * (j4q_upload_bf16). J4Q_GEMM_INT8 (Q8_0 weights) quantizes X per 32 and runs int8 MFMA;
+ * J4Q_GEMM_BF16 (Q8_0, Q4_0 with cols % 128 == 0, Q4_K, Q6_K) runs bf16 MFMA on W
+ * dequantized to bf16 from LDS-staged blocks. Other types or variants: J4Q_EUNSUPPORTED. */
 int j4q_quant_matmul(j4q_buffer weights, j4q_buffer x, int variant, j4q_buffer *y);
 
 /* ---- stream-ordered entry points on caller memory (no sync) ----------------------------- */
@@ -179,9 +181,9 @@ int j4q_quant_matmul(j4q_buffer weights, j4q_buffer x, int variant, j4q_buffer *
  * hipFreeAsync, batch x rows x windows floats); nothing else is allocated. */
 int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *add_dev, float *y_dev,
                           int64_t batch, void *stream);
-/* Prefill GEMM into caller memory. x_dev bf16 [m, cols]; y_dev fp32 [m, rows]. The int8
- * variant also needs xq_dev int8 [m, cols] and xs_dev fp32 [m, cols/32] as workspace;
- * the bf16 variant ignores them. */
+/* Prefill GEMM into caller memory (the weight types and variants of j4q_quant_matmul).
+ * x_dev bf16 [m, cols]; y_dev fp32 [m, rows]. The int8 variant also needs xq_dev int8
+ * [m, cols] and xs_dev fp32 [m, cols/32] as workspace; the bf16 variant ignores them. */
 int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, int8_t *xq_dev,
                           float *xs_dev, float *y_dev, void *stream);
 

@@ -8,7 +8,7 @@ same argument meaning and error types. Every operation runs the engine's HIP ker
 ``libjax4j_mi355x.so``; nothing here computes on the CPU.
 
 Engine-local extensions (no SPI counterpart): batched ``quant_matvec`` over x [B, K],
-``quant_matmul`` (prefill GEMM, Q8_0 weights x bf16 activations), ``quantize_act``,
+``quant_matmul`` (prefill GEMM, Q8_0 / Q4_0 / Q4_K / Q6_K weights x bf16 activations), ``quantize_act``,
 ``dequantize`` and ``export_quantized``.
 """
 from __future__ import annotations
@@ -195,7 +195,8 @@ class Mi355xBackend:
 
     # ---- engine-local extensions ----------------------------------------------------------
     def quant_matmul(self, weights: DeviceBuffer, x: DeviceBuffer, variant: str = "int8") -> DeviceBuffer:
-        """Prefill GEMM Y[M, N] = X[M, K] . W^T for Q8_0 W and bf16 X."""
+        """Prefill GEMM Y[M, N] = X[M, K] . W^T for bf16 X: "int8" over Q8_0 W, "bf16" over
+        Q8_0, Q4_0 (K % 128 == 0), Q4_K and Q6_K W (quantMatvec per row of X)."""
         v = {"int8": N.GEMM_INT8, "bf16": N.GEMM_BF16}.get(variant)
         if v is None:
             raise IllegalArgumentException(f"unknown GEMM variant {variant!r}")

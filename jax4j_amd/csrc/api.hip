@@ -374,6 +374,23 @@ bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0;
 
 hipStream_t pick_stream(void *s) { return s ? (hipStream_t)s : g_stream; }
 
+// Weight types of the prefill GEMM: Q8_0 for both variants; Q4_0 (cols % 128 == 0), Q4_K
+// and Q6_K for the bf16 variant (the int8 variant folds one Q8_0 scale per 32-block).
+int check_gemm_weights(const Buf &w, int variant, const char *op) {
+    if (w.qtype == J4Q_Q8_0) return J4Q_OK;
+    if (variant == J4Q_GEMM_INT8)
+        return fail(J4Q_EUNSUPPORTED, "%s: the int8 variant needs Q8_0 weights, got type %d (use the bf16 variant)", op,
+                    w.qtype);
+    if (!j4q::gemm_kq_supported(w.qtype, w.dims[1]))
+        return fail(J4Q_EUNSUPPORTED, "%s: no GEMM for type %d with %lld columns (Q8_0, Q4_0 with cols %% 128 == 0, Q4_K, Q6_K)",
+                    op, w.qtype, (long long)w.dims[1]);
+    return J4Q_OK;
+}
+
+hipError_t launch_gemm_bf16(const Buf &w, const j4q::QMat &m, const uint16_t *x, float *y, int64_t rows, hipStream_t s) {
+    return w.qtype == J4Q_Q8_0 ? j4q::launch_gemm_q8_bf16(m, x, y, rows, s) : j4q::launch_gemm_kq_bf16(w.qtype, m, x, y, rows, s);
+}
+
 }  // namespace
 
 namespace j4q {
@@ -765,7 +782,7 @@ int j4q_quant_matmul(j4q_buffer wh, j4q_buffer xh, int variant, j4q_buffer *out)
     int rc;
     if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatmul", &w))) return rc;
     if ((rc = get_buf(xh, J4Q_KIND_BF16, "quantMatmul", &x))) return rc;
-    if (w->qtype != J4Q_Q8_0) return fail(J4Q_EUNSUPPORTED, "quantMatmul: only Q8_0 weights are supported, got type %d", w->qtype);
+    if ((rc = check_gemm_weights(*w, variant, "quantMatmul"))) return rc;
     if (x->rank != 2 || x->dims[1] != w->dims[1] || x->dims[0] <= 0)
         return fail(J4Q_EINVAL, "quantMatmul shape mismatch: [%lld, %lld] x [%lld, %lld]", (long long)w->dims[0],
                     (long long)w->dims[1], (long long)x->dims[0], (long long)(x->rank == 2 ? x->dims[1] : 0));
@@ -777,7 +794,7 @@ int j4q_quant_matmul(j4q_buffer wh, j4q_buffer xh, int variant, j4q_buffer *out)
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, 2, M, N, (uint64_t)(M * N) * 4, out, &ydev))) return rc;
     if (variant == J4Q_GEMM_BF16) {
-        LAUNCH_INTO("quantMatmul", out, j4q::launch_gemm_q8_bf16(m, xdev, (float *)ydev, M, g_stream));
+        LAUNCH_INTO("quantMatmul", out, launch_gemm_bf16(*w, m, xdev, (float *)ydev, M, g_stream));
         return J4Q_OK;
     }
     void *ws = nullptr;
@@ -839,13 +856,13 @@ int j4q_quant_matmul_into(j4q_buffer wh, const uint16_t *x, int64_t m, int varia
     Buf *w;
     int rc;
     if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatmul_into", &w))) return rc;
-    if (w->qtype != J4Q_Q8_0) return fail(J4Q_EUNSUPPORTED, "quantMatmul_into: only Q8_0 weights are supported");
+    if ((rc = check_gemm_weights(*w, variant, "quantMatmul_into"))) return rc;
     if ((rc = check_gemm_size(m, w->dims[1], variant, "quantMatmul_into"))) return rc;
     if ((rc = ensure_ready())) return rc;
     const hipStream_t s = pick_stream(stream);
     const j4q::QMat mm = qmat_of(*w);
     if (variant == J4Q_GEMM_BF16) {
-        HIP_TRY("quantMatmul_into", j4q::launch_gemm_q8_bf16(mm, x, y, m, s));
+        HIP_TRY("quantMatmul_into", launch_gemm_bf16(*w, mm, x, y, m, s));
         return J4Q_OK;
     }
     HIP_TRY("quantMatmul_into", j4q::launch_quantize_act(x, m, mm.cols, xq, xs, s));
@@ -863,7 +880,7 @@ int j4q_quant_matmul_noalloc(j4q_buffer wh, const uint16_t *x, int64_t m, int va
     Buf *w;
     int rc;
     if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatmul_noalloc", &w))) return rc;
-    if (w->qtype != J4Q_Q8_0) return fail(J4Q_EUNSUPPORTED, "quantMatmul_noalloc: only Q8_0 weights are supported");
+    if ((rc = check_gemm_weights(*w, variant, "quantMatmul_noalloc"))) return rc;
     const int64_t K = w->dims[1];
     if ((rc = check_gemm_size(m, K, variant, "quantMatmul_noalloc"))) return rc;
     if (variant == J4Q_GEMM_INT8 && (uint64_t)m * (uint64_t)K > kScratchQBytes)
@@ -874,7 +891,7 @@ int j4q_quant_matmul_noalloc(j4q_buffer wh, const uint16_t *x, int64_t m, int va
     const hipStream_t s = pick_stream(stream);
     const j4q::QMat mm = qmat_of(*w);
     if (variant == J4Q_GEMM_BF16) {
-        HIP_TRY("quantMatmul_noalloc", j4q::launch_gemm_q8_bf16(mm, x, y, m, s));
+        HIP_TRY("quantMatmul_noalloc", launch_gemm_bf16(*w, mm, x, y, m, s));
         return J4Q_OK;
     }
     int8_t *xq = (int8_t *)g_scratch;

@@ -269,7 +269,7 @@ def test_gemm_into_caller_memory_matches(backend):
 def test_gemm_errors(backend):
     w4 = backend.upload_quantized(S.quant_blocks(QuantType.Q4_0, 3, 8, 64), QuantType.Q4_0, (8, 64))
     x = backend.upload(S.activations_bf16(4, 2 * 64).reshape(2, 64), shape=(2, 64), dtype=DType.BF16)
-    with pytest.raises(IllegalArgumentException, match="only Q8_0"):
+    with pytest.raises(IllegalArgumentException, match="int8 variant needs Q8_0"):
         backend.quant_matmul(w4, x, "int8")
     w8 = backend.upload_quantized(S.quant_blocks(QuantType.Q8_0, 3, 8, 96), QuantType.Q8_0, (8, 96))
     with pytest.raises(IllegalArgumentException, match="shape mismatch"):
