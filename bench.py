@@ -343,10 +343,11 @@ def decode_workload(eng: Engine, model: DecodeModel, batch: int, steps: int, war
     }
 
 
-def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n: int = 4096, k: int = 4096):
+def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n: int = 4096, k: int = 4096,
+                  qt: QuantType = QuantType.Q8_0):
     """Q8_0 prefill GEMM Y[m, n] = X[m, k] . W^T with bf16 X; the int8 variant's
-    timed call includes quantizing X (j4q_quant_matmul_into runs both kernels)."""
-    qt = QuantType.Q8_0
+    timed call includes quantizing X (j4q_quant_matmul_into runs both kernels). With another
+    `qt` (Q4_0, Q4_K, Q6_K; bf16 variant) the same GEMM over configs[1]/[2]'s matrices."""
     blob_bytes = qt.byte_size_for(n * k)
     copies = max(1, math.ceil(ROTATE_BYTES / blob_bytes))
     ws = [eng.weights(qt, n, k, 0x5EED8 + 31 * i)[0] for i in range(copies)]
@@ -376,10 +377,12 @@ def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n:
     for p in (x, xq, xs, y):
         eng.hip.free(p)
     st = stats_us(sms, cnt)
-    log(f"gemm {variant} M={m}: {per * 1e3:.2f} us (median {st['median_us']}), {tops:.0f} TOPS "
+    name = f"{qt.name.lower()}_gemm_{variant}_m{m}" + ("" if qt == QuantType.Q8_0 else f"_n{n}_k{k}")
+    log(f"{name}: {per * 1e3:.2f} us (median {st['median_us']}), {tops:.0f} TOPS "
         f"({100 * tops / INT8_PEAK_TOPS:.1f}% of int8 peak, {100 * tops / peak:.1f}% of {variant} peak)")
     return {
-        "workload": f"q8_0_gemm_{variant}_m{m}",
+        "workload": name,
+        "quant": qt.name,
         "variant": variant,
         "M": m,
         "N": n,
@@ -467,10 +470,58 @@ def summarize_timeline(name, ms_per_launch, rec, ticks_per_us):
 CALIBRATION_BYTES = [17858560, 25422848, 33103872, 48242688, 66060288, 430940160]
 
 
+def torch_sum_reader(sizes, steps: int, warmup: int) -> None:
+    """An independent reader (--torch-reader): torch.sum over rotating fp32 tensors of each size
+    (at least ROTATE_BYTES of copies, as the GEMV workloads rotate), PyTorch's own reduction
+    kernel, timed with events on torch's stream; prints one JSON list. It runs in a process of
+    its own that never loads the engine: PyTorch's wheel ships its own HIP and HSA runtimes,
+    and a process holding both those and the engine's (ROCm's) crashed under rocprofv3 at
+    torch's first kernel launch. A Python loop launches the sums, so the events include any
+    host gap between launches; the rocprofv3 kernel trace gives the kernel durations alone."""
+    import torch
+
+    out = []
+    for nb in sizes:
+        copies = max(1, math.ceil(ROTATE_BYTES / nb))
+        bufs = [torch.ones(nb // 4, device="cuda") for _ in range(copies)]
+        outs = torch.empty(copies, device="cuda")
+        for i in range(warmup):
+            torch.sum(bufs[i % copies], dim=0, out=outs[i % copies])
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(steps):
+            torch.sum(bufs[i % copies], dim=0, out=outs[i % copies])
+        b.record()
+        torch.cuda.synchronize()
+        us = 1e3 * a.elapsed_time(b) / steps
+        del bufs
+        out.append({"bytes": nb, "copies": copies, "us_per_launch": round(us, 3),
+                    "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+                    "note": "event-timed Python loop: an upper bound on the kernel time"})
+    print(json.dumps(out), flush=True)
+
+
+def run_torch_reader(sizes, steps: int, warmup: int):
+    """torch_sum_reader in a child process (see there); its JSON list, or None if it failed."""
+    import subprocess
+
+    cmd = [sys.executable, os.path.abspath(__file__), "--torch-reader", ",".join(map(str, sizes)),
+           "--steps", str(steps), "--warmup", str(warmup)]
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=600)
+    if proc.returncode != 0:
+        err = [l for l in proc.stderr.splitlines() if l.strip() and not l.startswith(("W20", "E20", "I20"))]
+        log(f"warning: torch reader exited with {proc.returncode}: " + " | ".join(err[-6:]))
+        return None
+    return json.loads(proc.stdout.strip().splitlines()[-1])
+
+
 def calibrate(eng: Engine, steps: int, warmup: int):
     """The practical HBM read ceiling of one launch of each size (j4q_stream_read over rotating
-    buffers, so the Infinity Cache cannot serve them), and a copy kernel of known size so a
-    counter profile of this process can scale the GEMV's byte counters."""
+    buffers, so the Infinity Cache cannot serve them: 1 or 2 workgroups per CU, 4 or 8 1 KB
+    loads in flight per wave), PyTorch's torch.sum over the same sizes as an independent
+    reader, and a copy kernel of known size so a counter profile of this process can scale
+    the GEMV's byte counters."""
     out = []
     for nbytes in CALIBRATION_BYTES:
         nb = (nbytes + 15) // 16 * 16
@@ -478,12 +529,12 @@ def calibrate(eng: Engine, steps: int, warmup: int):
         bufs = [eng.hip.malloc(nb) for _ in range(copies)]
         sink = eng.hip.malloc(4 * 4 * eng.info["compute_units"])
         row = {"workload": f"stream_read_{nb}", "bytes": nb, "copies": copies}
-        for wpc in (1, 2):
+        for wpc, depth in ((1, 4), (2, 4), (1, 8), (2, 8)):
             fn = eng.lib.j4q_stream_read
             s = C.c_void_p(eng.stream)
 
             def enqueue(i):
-                rc = fn(C.c_void_p(bufs[i % copies]), nb, C.c_void_p(sink), wpc, s)
+                rc = fn(C.c_void_p(bufs[i % copies]), nb, C.c_void_p(sink), wpc, depth, s)
                 if rc:
                     check(rc, "stream_read")
 
@@ -491,14 +542,18 @@ def calibrate(eng: Engine, steps: int, warmup: int):
             ms, _, _, _, _ = eng.time_region(enqueue, steps)
             _, sms, cnt, _, _ = eng.time_region(enqueue, steps, 30.0, SAMPLES)
             st = stats_us(sms, cnt)
-            row[f"wg_per_cu_{wpc}"] = {"us_per_launch": round(1e3 * ms / steps, 3), "sampled": st,
-                                       "GBps": round(nb / (ms / steps * 1e-3) / 1e9, 1)}
+            row[f"wg_per_cu_{wpc}_depth_{depth}"] = {"us_per_launch": round(1e3 * ms / steps, 3), "sampled": st,
+                                                     "GBps": round(nb / (ms / steps * 1e-3) / 1e9, 1)}
         for b in bufs + [sink]:
             eng.hip.free(b)
-        best = max(row["wg_per_cu_1"]["GBps"], row["wg_per_cu_2"]["GBps"])
+        best = max(v["GBps"] for k, v in row.items() if k.startswith("wg_per_cu"))
         row["best_GBps"] = best
         log(f"stream_read {nb / 1e6:.1f} MB: {best:.0f} GB/s ({100 * best / HBM_PEAK_GBS:.1f}% of HBM peak)")
         out.append(row)
+    sums = run_torch_reader([r["bytes"] for r in out], steps, warmup)
+    for row, t in zip(out, sums or []):
+        row["torch_sum"] = t
+        log(f"torch.sum {row['bytes'] / 1e6:.1f} MB: {t['GBps']:.0f} GB/s (event-timed, separate process)")
     n = 256 << 20
     src, dst = eng.hip.malloc(n), eng.hip.malloc(n)
     for _ in range(3):
@@ -641,10 +696,16 @@ def main():
     ap.add_argument("--batches", default="4,8,16", help="comma list of batch sizes for the batched decode-step lines")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the streaming-read ceiling and a copy kernel of known size (counter scaling)")
+    ap.add_argument("--torch-reader", default="", metavar="BYTES,...",
+                    help="only run PyTorch's torch.sum over rotating tensors of these sizes, in this process "
+                         "(--calibrate runs it as a child process)")
     ap.add_argument("--timeline", action="store_true",
                     help="also record the per-wave timeline of one launch of the dominant GEMV and of the step's "
                          "smaller B = 1 GEMVs (j4q_gemv_trace)")
     args = ap.parse_args()
+    if args.torch_reader:
+        torch_sum_reader([int(b) for b in args.torch_reader.split(",") if b], args.steps, args.warmup)
+        return
     if args.gpus != 1:
         print(
             f"bench.py: this engine is measured on one GPU; --gpus {args.gpus} is not supported "
@@ -692,6 +753,11 @@ def main():
             for m in (32, 128, 512, 2048):
                 for variant in ("int8", "bf16"):
                     others.append(gemm_workload(eng, m, variant, args.steps, args.warmup))
+            # the prefill GEMM over the K-quant matrices of configs[2] and the Q4_0 one of configs[1]
+            for qt, n, k in ((Q4K, 14336, 4096), (Q6K, 4096, 14336), (QuantType.Q4_0, 11008, 4096)):
+                for m in ((32, 512, 2048) if qt != QuantType.Q4_0 else (512,)):
+                    others.append(gemm_workload(eng, m, "bf16", max(2, args.steps // 2), max(1, args.warmup // 2),
+                                                n=n, k=k, qt=qt))
 
     cpu, cpu_all = (None, None) if (args.quick or args.only) else cpu_rows(args.cpu_seconds)
     achieved = dominant["GBps"]

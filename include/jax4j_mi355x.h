@@ -320,8 +320,10 @@ int j4q_copy(void *device_dst, const void *device_src, uint64_t nbytes, void *st
  * non-temporal loads, each wave one contiguous segment, and writes nothing but, in a case no
  * input produces in practice, one word per workgroup to `sink` (workgroups_per_cu x CUs
  * words): the practical HBM read ceiling of a single launch of that size, against which the
- * GEMV launches are measured. 1..4 workgroups of 512 threads per CU. */
-int j4q_stream_read(const void *device_src, uint64_t nbytes, uint32_t *sink, int32_t workgroups_per_cu, void *stream);
+ * GEMV launches are measured. 1..4 workgroups of 512 threads per CU; each wave keeps
+ * loads_in_flight (4 or 8) 1 KB loads in flight. */
+int j4q_stream_read(const void *device_src, uint64_t nbytes, uint32_t *sink, int32_t workgroups_per_cu,
+                    int32_t loads_in_flight, void *stream);
 /* Per-wave timeline of the batch-1 vector-ALU GEMV launches enqueued while it is set:
  * wave w < n_words / 4 writes device_words[4 w .. 4 w + 3] = {wall clock (the device's
  * constant-rate clock, hipDeviceAttributeWallClockRate) at entry, after x is staged, after

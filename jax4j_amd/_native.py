@@ -158,7 +158,7 @@ SIGNATURES = {
     "j4q_gguf_upload": [_u64, _i64, _pbuf],
     "j4q_spin": [C.c_uint32, _vp],
     "j4q_copy": [_vp, _vp, _u64, _vp],
-    "j4q_stream_read": [_vp, _u64, _vp, _i32, _vp],
+    "j4q_stream_read": [_vp, _u64, _vp, _i32, _i32, _vp],
     "j4q_gemv_trace": [_vp, _i64],
 }
 _RESTYPES = {"j4q_last_error": C.c_char_p}

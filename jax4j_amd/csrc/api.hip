@@ -964,8 +964,11 @@ int j4q_spin(uint32_t microseconds, void *stream) {
     return J4Q_OK;
 }
 
-int j4q_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int32_t workgroups_per_cu, void *stream) {
+int j4q_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int32_t workgroups_per_cu, int32_t loads_in_flight,
+                    void *stream) {
     if (!src || !sink) return fail(J4Q_EINVAL, "stream_read: NULL pointer");
+    if (loads_in_flight != 4 && loads_in_flight != 8)
+        return fail(J4Q_EINVAL, "stream_read: loads_in_flight %d is not 4 or 8", loads_in_flight);
     if (nbytes % 16 != 0 || !aligned(src, 16) || nbytes >= 0x80000000ull)
         return fail(J4Q_EINVAL, "stream_read: nbytes must be a multiple of 16 below 2 GiB, src 16-byte aligned");
     if (workgroups_per_cu < 1 || workgroups_per_cu > 4) return fail(J4Q_EINVAL, "stream_read: workgroups_per_cu %d out of range [1, 4]", workgroups_per_cu);
@@ -974,7 +977,8 @@ int j4q_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int32_t wo
     if (rc) return rc;
     hipDeviceProp_t p;
     HIP_TRY("hipGetDeviceProperties", hipGetDeviceProperties(&p, g_dev));
-    HIP_TRY("stream_read", j4q::launch_stream_read(src, nbytes, sink, workgroups_per_cu * p.multiProcessorCount, pick_stream(stream)));
+    HIP_TRY("stream_read", j4q::launch_stream_read(src, nbytes, sink, workgroups_per_cu * p.multiProcessorCount,
+                                                   loads_in_flight, pick_stream(stream)));
     return J4Q_OK;
 }
 

@@ -152,7 +152,7 @@ hipError_t launch_synth_f32(uint64_t seed, int64_t n, float *out, hipStream_t s)
 hipError_t launch_synth_bf16(uint64_t seed, int64_t n, uint16_t *out, hipStream_t s);
 hipError_t launch_spin(uint32_t microseconds, int wall_clock_khz, hipStream_t s);
 hipError_t launch_copy(void *dst, const void *src, uint64_t nbytes, hipStream_t s);
-// grid workgroups of 512 threads; sink holds `grid` words (written only in a case no input
-// produces in practice)
-hipError_t launch_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int grid, hipStream_t s);
+// grid workgroups of 512 threads, `depth` (4 or 8) 1 KB loads in flight per wave; sink holds
+// `grid` words (written only in a case no input produces in practice)
+hipError_t launch_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int grid, int depth, hipStream_t s);
 }  // namespace j4q

@@ -413,12 +413,13 @@ hipError_t launch_copy(void *dst, const void *src, uint64_t nbytes, hipStream_t 
 }
 
 // Read-only streaming probe: wave w of the grid reads its own contiguous segment of `seg`
-// bytes (a multiple of 4 KB) with 128-bit non-temporal buffer loads, 1 KB per load
-// instruction and four in flight, and writes nothing but a per-workgroup value no input
+// bytes (a multiple of U KB) with 128-bit non-temporal buffer loads, 1 KB per load
+// instruction and U in flight, and writes nothing but a per-workgroup value no input
 // produces in practice (so the loads cannot be dropped). Offsets past nbytes are out of the
 // buffer resource's range: those loads return zeros without touching memory. It measures
 // the practical HBM read ceiling of one launch of a given size: the same dispatch, ramp and
 // tail a GEMV launch of that many bytes pays.
+template <int U>
 __global__ void __launch_bounds__(512) stream_read_kernel(const void *src, uint32_t nbytes, uint32_t seg,
                                                           uint32_t *__restrict__ sink) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(src), (short)0, (int)nbytes, 0x00020000);
@@ -426,24 +427,27 @@ __global__ void __launch_bounds__(512) stream_read_kernel(const void *src, uint3
     const uint32_t w = blockIdx.x * 8u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t base = w * seg + lane * 16u;
     uint32_t acc = 0;
-    for (uint32_t off = 0; off < seg; off += 4096u) {
-        cu32x4 v[4];
+    for (uint32_t off = 0; off < seg; off += 1024u * U) {
+        cu32x4 v[U];
 #pragma unroll
-        for (int u = 0; u < 4; u++)
+        for (int u = 0; u < U; u++)
             v[u] = __builtin_bit_cast(cu32x4, __builtin_amdgcn_raw_buffer_load_b128(r, base + off + 1024u * u, 0, 2));
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
     if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
 }
 
-// nbytes < 2^31 (32-bit buffer offsets; the caller checks).
-hipError_t launch_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int grid, hipStream_t s) {
+// nbytes < 2^31 (32-bit buffer offsets; the caller checks); loads in flight 4 or 8.
+hipError_t launch_stream_read(const void *src, uint64_t nbytes, uint32_t *sink, int grid, int depth, hipStream_t s) {
     if (nbytes == 0) return hipSuccess;
-    if (nbytes >= 0x80000000ull || grid <= 0) return hipErrorInvalidValue;
-    const uint64_t waves = (uint64_t)grid * 8;
-    const uint64_t seg = (nbytes + waves * 4096 - 1) / (waves * 4096) * 4096;
-    stream_read_kernel<<<(unsigned)grid, 512, 0, s>>>(src, (uint32_t)nbytes, (uint32_t)seg, sink);
+    if (nbytes >= 0x80000000ull || grid <= 0 || (depth != 4 && depth != 8)) return hipErrorInvalidValue;
+    const uint64_t waves = (uint64_t)grid * 8, step = 1024ull * (uint64_t)depth;
+    const uint64_t seg = (nbytes + waves * step - 1) / (waves * step) * step;
+    if (depth == 8)
+        stream_read_kernel<8><<<(unsigned)grid, 512, 0, s>>>(src, (uint32_t)nbytes, (uint32_t)seg, sink);
+    else
+        stream_read_kernel<4><<<(unsigned)grid, 512, 0, s>>>(src, (uint32_t)nbytes, (uint32_t)seg, sink);
     return hipGetLastError();
 }
 
