@@ -387,8 +387,10 @@ int check_gemm_weights(const Buf &w, int variant, const char *op) {
     return J4Q_OK;
 }
 
-hipError_t launch_gemm_bf16(const Buf &w, const j4q::QMat &m, const uint16_t *x, float *y, int64_t rows, hipStream_t s) {
-    return w.qtype == J4Q_Q8_0 ? j4q::launch_gemm_q8_bf16(m, x, y, rows, s) : j4q::launch_gemm_kq_bf16(w.qtype, m, x, y, rows, s);
+// Takes the weight type by value: callers read it before alloc_buf, whose registration of the
+// output can move the buffer table (and every Buf pointer into it).
+hipError_t launch_gemm_bf16(int qtype, const j4q::QMat &m, const uint16_t *x, float *y, int64_t rows, hipStream_t s) {
+    return qtype == J4Q_Q8_0 ? j4q::launch_gemm_q8_bf16(m, x, y, rows, s) : j4q::launch_gemm_kq_bf16(qtype, m, x, y, rows, s);
 }
 
 }  // namespace
@@ -790,11 +792,13 @@ int j4q_quant_matmul(j4q_buffer wh, j4q_buffer xh, int variant, j4q_buffer *out)
     if ((rc = ensure_ready())) return rc;
     const int64_t M = x->dims[0], N = w->dims[0], K = w->dims[1];
     const j4q::QMat m = qmat_of(*w);
+    const int qt = w->qtype;
     const uint16_t *xdev = (const uint16_t *)x->dev;
+    // w and x are not used past this point: registering y below may move the buffer table
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, 2, M, N, (uint64_t)(M * N) * 4, out, &ydev))) return rc;
     if (variant == J4Q_GEMM_BF16) {
-        LAUNCH_INTO("quantMatmul", out, launch_gemm_bf16(*w, m, xdev, (float *)ydev, M, g_stream));
+        LAUNCH_INTO("quantMatmul", out, launch_gemm_bf16(qt, m, xdev, (float *)ydev, M, g_stream));
         return J4Q_OK;
     }
     void *ws = nullptr;
@@ -862,7 +866,7 @@ int j4q_quant_matmul_into(j4q_buffer wh, const uint16_t *x, int64_t m, int varia
     const hipStream_t s = pick_stream(stream);
     const j4q::QMat mm = qmat_of(*w);
     if (variant == J4Q_GEMM_BF16) {
-        HIP_TRY("quantMatmul_into", launch_gemm_bf16(*w, mm, x, y, m, s));
+        HIP_TRY("quantMatmul_into", launch_gemm_bf16(w->qtype, mm, x, y, m, s));
         return J4Q_OK;
     }
     HIP_TRY("quantMatmul_into", j4q::launch_quantize_act(x, m, mm.cols, xq, xs, s));
@@ -891,7 +895,7 @@ int j4q_quant_matmul_noalloc(j4q_buffer wh, const uint16_t *x, int64_t m, int va
     const hipStream_t s = pick_stream(stream);
     const j4q::QMat mm = qmat_of(*w);
     if (variant == J4Q_GEMM_BF16) {
-        HIP_TRY("quantMatmul_noalloc", launch_gemm_bf16(*w, mm, x, y, m, s));
+        HIP_TRY("quantMatmul_noalloc", launch_gemm_bf16(w->qtype, mm, x, y, m, s));
         return J4Q_OK;
     }
     int8_t *xq = (int8_t *)g_scratch;

@@ -243,6 +243,27 @@ def test_gemm_full_size_rows_and_variants_agree(backend, m):
         backend.release(h)
 
 
+@pytest.mark.parametrize("qt", [QuantType.Q8_0, QuantType.Q4_K], ids=lambda q: q.name)
+def test_gemm_while_the_buffer_table_grows(backend, qt):
+    """Regression: j4q_quant_matmul registers its output after looking up W and X, and that
+    registration can move the engine's buffer table. The bf16 dispatch once read W's type
+    through the stale pointer and failed with 'invalid argument' whenever the table grew on
+    that call. Here 300 calls keep their outputs alive, so the table grows many times during
+    a call; every call must succeed and equal the first bit for bit."""
+    m, n, k = 96, 64, 256
+    note("gemm while the table grows", qt.name)
+    w_blob = S.quant_blocks(qt, 77, n, k)
+    xb = S.activations_bf16(78, m * k).reshape(m, k)
+    w = backend.upload_quantized(w_blob, qt, (n, k))
+    x = backend.upload(xb, shape=(m, k), dtype=DType.BF16)
+    ys = [backend.quant_matmul(w, x, "bf16") for _ in range(300)]
+    first = bits(backend.download(ys[0]).reshape(m, n))
+    for y in (ys[1], ys[127], ys[128], ys[255], ys[256], ys[-1]):
+        assert np.array_equal(bits(backend.download(y).reshape(m, n)), first)
+    for h in ys + [w, x]:
+        backend.release(h)
+
+
 def test_gemm_into_caller_memory_matches(backend):
     """j4q_quant_matmul_into on engine-owned device memory gives the allocating call's result."""
     m, n, k = 70, 160, 512
