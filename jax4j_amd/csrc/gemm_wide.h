@@ -281,6 +281,10 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void *lds, uint32
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4, vo, 0, 0, 0);
 }
 
+__device__ __forceinline__ void dma4s(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t vo, uint32_t so) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 4, vo, so, 0, 0);
+}
+
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt not waited for).
 template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
@@ -1069,6 +1073,194 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
     for (int j = 0; j < 4; j++) {
         const int row = m0 + 4 * g + j;
         if (row < M && col < N) y[(int64_t)row * N + col] = ((acc[j] + p1[j]) + p2[j]) + p3[j];
+    }
+}
+
+}  // namespace gw
+}  // namespace j4q
+
+namespace j4q {
+namespace gw {
+
+// Prefill GEMM, int8 variant with the tiles loaded straight into LDS and the fold of each
+// block pair overlapped with the next pair's products: the same arithmetic as gemm_i8_wide
+// (every output folded by one lane over all of K in block order, fma(float(I_b),
+// fl(sx * dw), acc)), so results are bit-identical to it and to the oracle's emulation.
+//  - Tile 64 x 128 per workgroup of 8 waves (two per SIMD); wave w owns the 32 x 32 outputs
+//    of rows 32 (w % 2), columns 32 (w / 2). K advances in stages of four blocks.
+//  - Every stage moves straight from global memory into one of three LDS stage buffers
+//    (buffer_load ... lds, no VGPRs, no LDS stores): X as 64 rows x 128 bytes and W as 128
+//    rows x 128 bytes (16-byte chunk c of row r at slot c ^ ((r / 2) % 8), so the rows of an
+//    operand read spread over the banks), then sx as [64 rows][4 blocks] fp32 and dw as
+//    [4 blocks][128 columns] fp16 (from the block-major copy). A lane loads the global chunk
+//    that belongs at its LDS slot. Every wave issues exactly four loads per stage (X, two W,
+//    a quarter of sx or of dw), so all waves wait for the same count and no load sits behind
+//    a branch.
+//  - Iteration i: wait for own stage-i loads, barrier, load stage i + 2 into the buffers of
+//    stage i - 1 (the ring's look-ahead past the end loads the last stage again), then per
+//    block pair: read its operands, issue its two int8 products and its scale-product MFMA,
+//    and fold the pair before it (still in registers) while the matrix core runs, so the
+//    vector-ALU work of one pair overlaps the matrix work of the next in every wave.
+// Requires K % 32 == 0, N % 8 == 0, M * K < 2^31 and N * K < 2^31.
+template <int SCHED>
+__global__ void __launch_bounds__(512)
+gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc, float *__restrict__ y, int M) {
+    constexpr int BM = 64, BN = 128, SB = 4;
+    constexpr int kX = BM * 128, kW = BN * 128, kSx = BM * SB * 4, kS = kSx + SB * BN * 2;
+    __shared__ __attribute__((aligned(1024))) uint8_t xs0[kX], xs1[kX], xs2[kX];
+    __shared__ __attribute__((aligned(1024))) uint8_t ws0[kW], ws1[kW], ws2[kW];
+    __shared__ __attribute__((aligned(1024))) uint8_t ss0[kS], ss1[kS], ss2[kS];
+    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32;
+    const int nfull = nblk / SB, ns = (nblk + SB - 1) / SB;  // full stages, all stages
+    const int mt = (M + BM - 1) / BM;
+    // Workgroup b runs on XCD b % 8; each XCD takes a contiguous range of tiles (m fastest),
+    // so the m tiles of the same W rows share an L2.
+    const int total = (int)gridDim.x;
+    int tile = (int)blockIdx.x;
+    if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
+
+    const int lane = (int)threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wm = wave & 1, wn = wave >> 1, h = lane >> 5, l32 = lane & 31;
+
+    // X: wave w fills rows 8 w .. 8 w + 7 (lane L the slot L % 8 of row 8 w + L / 8); W:
+    // load j of wave w fills rows 8 (8 j + w) .. + 7.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xq, (uint64_t)M * (uint64_t)K);
+    uint32_t xoff;
+    {
+        const int row = 8 * wave + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+        xoff = m0 + row < M ? (uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)c * 16u : kOob;
+    }
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
+    uint32_t woff[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int row = 8 * (8 * j + wave) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+        woff[j] = n0 + row < N ? (uint32_t)(n0 + row) * (uint32_t)K + (uint32_t)c * 16u : kOob;
+    }
+    // Scales, 4 bytes per lane into 256-byte slot w of the stage's scale buffer:
+    //  - waves 0..3: sx as [64 rows][4 blocks] fp32; wave q lane L: row 16 q + L / 4, block
+    //    L % 4 of the stage;
+    //  - waves 4..7: dw as [4 blocks][128 columns] fp16; wave 4 + q lane L: block q of the
+    //    stage, columns 2 L and 2 L + 1 (N % 8 == 0 keeps the pair in range together).
+    // Each wave picks its source (resource, lane offset, bytes per stage) once.
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(xsc, (uint64_t)M * (uint64_t)nblk * 4u);
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
+    const bool sxw = wave < 4;
+    const __amdgpu_buffer_rsrc_t cr = sxw ? sr : dr;
+    uint32_t coff;
+    {
+        const int q = wave & 3, row = 16 * q + (lane >> 2), col = n0 + 2 * lane;
+        coff = sxw ? (m0 + row < M ? (uint32_t)(m0 + row) * (uint32_t)nblk * 4u + (uint32_t)(lane & 3) * 4u : kOob)
+                   : (col < N ? ((uint32_t)q * (uint32_t)N + (uint32_t)col) * 2u : kOob);
+    }
+    const uint32_t cstep = sxw ? 4u * SB : (uint32_t)N * 2u * SB;  // bytes per stage
+
+    // Loads of stage i (clamped to the last stage, which the ring's look-ahead past the end
+    // reads again: in range, never computed on).
+    auto load = [&](int i, uint8_t *xb, uint8_t *wb, uint8_t *sb) {
+        const uint32_t st = (uint32_t)(i < ns ? i : ns - 1);
+        dma16(xr, xb + wave * 1024, xoff, st * (SB * 32u));
+        dma16(wr, wb + wave * 1024, woff[0], st * (SB * 32u));
+        dma16(wr, wb + (8 + wave) * 1024, woff[1], st * (SB * 32u));
+        dma4s(cr, sb + wave * 256, coff, st * cstep);
+    };
+
+    const int ra = 32 * wm + l32, rb = 32 * wn + l32;
+    const int asw = (ra >> 1) & 7, bsw = (rb >> 1) & 7;
+    float acc[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.f;
+    // result element v: row 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32
+    auto fold = [&](const i32x16 &I, const f32x32 &P, int e) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], P[16 * e + v], acc[v]);
+    };
+    // products of block pair p of a stage (blocks 2 p, 2 p + 1) and their scale products:
+    // lane (h, l32) supplies sx of row ra and dw of column rb for block 2 p + h, and
+    // v_mfma_f32_32x32x1_2b_f32 returns both 32 x 32 outer products (block 2 p in elements
+    // 0..15, 2 p + 1 in 16..31) in the layout of the int8 products
+    struct Pair {
+        i32x16 I0, I1;
+        f32x32 P;
+    };
+    auto products = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *sb, int p, Pair &out) {
+        const int c0 = 4 * p + h, c1 = 4 * p + 2 + h;  // chunks of blocks 2 p and 2 p + 1
+        const i32x4 a0 = *reinterpret_cast<const i32x4 *>(xb + ra * 128 + ((c0 ^ asw) << 4));
+        const i32x4 b0 = *reinterpret_cast<const i32x4 *>(wb + rb * 128 + ((c0 ^ bsw) << 4));
+        const i32x4 a1 = *reinterpret_cast<const i32x4 *>(xb + ra * 128 + ((c1 ^ asw) << 4));
+        const i32x4 b1 = *reinterpret_cast<const i32x4 *>(wb + rb * 128 + ((c1 ^ bsw) << 4));
+        const float sx = reinterpret_cast<const float *>(sb)[ra * SB + 2 * p + h];
+        const float dw = half_bits_to_float(reinterpret_cast<const uint16_t *>(sb + kSx)[(2 * p + h) * BN + rb]);
+        out.I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, i32x16{}, 0, 0, 0);
+        out.I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, i32x16{}, 0, 0, 0);
+        out.P = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dw, f32x32{}, 0, 0, 0);
+    };
+    // prev: the pair still to be folded; zeros before the first stage, whose fold adds exact
+    // zeros (fma(0, 0, +0) = +0)
+    Pair prev, cur;
+    prev.I0 = i32x16{};
+    prev.I1 = i32x16{};
+    prev.P = f32x32{};
+    // One full stage: pair 0's products with the fold of the pair before, then pair 1's
+    // products with the fold of pair 0; pair 1 stays pending for the next stage.
+    auto stage = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *sb) {
+        products(xb, wb, sb, 0, cur);
+        fold(prev.I0, prev.P, 0);
+        fold(prev.I1, prev.P, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        products(xb, wb, sb, 1, prev);
+        fold(cur.I0, cur.P, 0);
+        fold(cur.I1, cur.P, 1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto step = [&](int i, const uint8_t *xb, const uint8_t *wb, const uint8_t *sb, uint8_t *xn, uint8_t *wn,
+                    uint8_t *sn) {
+        wait_vm_lgkm0<4>();
+        lds_barrier();
+        load(i + 2, xn, wn, sn);
+        stage(xb, wb, sb);
+    };
+
+    load(0, xs0, ws0, ss0);
+    load(1, xs1, ws1, ss1);
+    int i = 0;
+    for (; i + 3 <= nfull; i += 3) {
+        step(i, xs0, ws0, ss0, xs2, ws2, ss2);
+        step(i + 1, xs1, ws1, ss1, xs0, ws0, ss0);
+        step(i + 2, xs2, ws2, ss2, xs1, ws1, ss1);
+    }
+    if (i < nfull) {
+        step(i, xs0, ws0, ss0, xs2, ws2, ss2);
+        i++;
+        if (i < nfull) {
+            step(i, xs1, ws1, ss1, xs0, ws0, ss0);
+            i++;
+        }
+    }
+    fold(prev.I0, prev.P, 0);
+    fold(prev.I1, prev.P, 1);
+    // a last stage of 1..3 blocks (in buffer i % 3)
+    if (nfull < ns) {
+        const int r = i % 3;
+        const uint8_t *xb = r == 0 ? xs0 : r == 1 ? xs1 : xs2;
+        const uint8_t *wb = r == 0 ? ws0 : r == 1 ? ws1 : ws2;
+        const uint8_t *sb = r == 0 ? ss0 : r == 1 ? ss1 : ss2;
+        __builtin_amdgcn_s_waitcnt(0);
+        lds_barrier();
+        const int nb = nblk - nfull * SB;
+        for (int p = 0; 2 * p < nb; p++) {
+            products(xb, wb, sb, p, cur);
+            fold(cur.I0, cur.P, 0);
+            if (2 * p + 1 < nb) fold(cur.I1, cur.P, 1);
+        }
+    }
+    const int col = n0 + rb;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int row = m0 + 32 * wm + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (row < M && col < N) y[(int64_t)row * N + col] = acc[v];
     }
 }
 
