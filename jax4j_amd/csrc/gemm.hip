@@ -418,7 +418,7 @@ hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs,
         } else {
             const int64_t tiles = ((m + 63) / 64) * ((w.rows + 127) / 128);
             if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-            gw::gemm_i8_lds<0><<<(unsigned)tiles, 512, 0, s>>>(w, xq, xs, y, (int)m);
+            gw::gemm_i8_lds<<<(unsigned)tiles, 512, 0, s>>>(w, xq, xs, y, (int)m);
         }
         return hipGetLastError();
     }

@@ -681,202 +681,14 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 
-// Prefill GEMM, int8 variant: Y[m, n] = sum over blocks b, in block order, of
+// Int8 variant of the prefill GEMM: Y[m, n] = sum over blocks b, in block order, of
 // fma(float(I_b[m, n]), fl(sx[m, b] * dw[n, b]), acc) with I_b the exact int32 dot of the
-// quantized activations and the Q8_0 quants of block b. Every output is folded by one lane
-// over all of K, so results are bit-identical to a sequential fp32 loop over the blocks.
-//
-// The scale products fl(sx * dw) come from the matrix core, one v_mfma_f32_32x32x1_2b_f32
-// outer product per two blocks, so the vector ALU does two operations per output and block
-// (convert, FMA) and each lane reads two scales per block pair from LDS instead of 17 per
-// block. Measured on MI355X (N = K = 4096, quantizer included), against the products on
-// the vector ALU: M = 512 45.8 us against 50.0, M = 2048 168 against 184.
-// Tile 64 x 128 per workgroup of 8 waves (two per SIMD); wave w owns the 32 x 32 outputs of
-// rows 32 (w % 2), columns 32 (w / 2), for all of K. K advances in stages of four blocks
-// (128 bytes of every row, one cache line):
-//  - X int8 (64 rows) and W int8 (128 rows) with whole-line loads, 128-bit LDS stores,
-//    16-byte chunk c of row r at chunk c ^ ((r / 2) % 8) of 128-byte rows, so the 16 rows of
-//    an operand read fall on distinct banks;
-//  - sx (the activation scales, [M][K / 32]): 16 bytes of each of the 64 rows per stage,
-//    loaded by wave 0 and stored block-major in LDS, so the 32 lanes that supply one
-//    block's sx to the scale-product MFMA read 32 consecutive floats;
-//  - dw from the block-major scale copy of the Q8_0 split layout, loaded by wave 1 and
-//    stored as fp32 in LDS.
-// Two LDS buffers and one barrier per stage; global loads run R stages ahead in a ring of
-// register sets. Requires K % 32 == 0, N % 8 == 0, M * K < 2^31 and N * K < 2^31.
-template <int R>
-__global__ void __launch_bounds__(512)
-gemm_i8_wide(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xs, float *__restrict__ y, int M) {
-    static_assert(R % 2 == 0 && R >= 2, "the ring unrolls by an even R");
-    constexpr int BM = 64, BN = 128, SB = 4;  // rows, columns, blocks per stage
-    constexpr int kXS = BM * 128, kWS = BN * 128, kSxS = SB * BM * 4, kDwS = SB * BN * 4;
-    constexpr int kBuf = kXS + kWS + kSxS + kDwS;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBuf];
-    const int N = (int)w.rows, K = (int)w.cols, nblk = K / 32, ns = (nblk + SB - 1) / SB;
-    const int mt = (M + BM - 1) / BM;
-    // Workgroup b runs on XCD b % 8; each XCD takes a contiguous range of tiles (m fastest),
-    // so the m tiles of the same W rows share an L2.
-    const int total = (int)gridDim.x;
-    int tile = (int)blockIdx.x;
-    if (total % 8 == 0) tile = (tile % 8) * (total / 8) + tile / 8;
-    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
-
-    const int tid = (int)threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1, h = lane >> 5, l32 = lane & 31;
-
-    // X: thread t stages 16-byte chunk t % 8 of tile row t / 8.
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xq, (uint64_t)M * (uint64_t)K);
-    const int xrow = tid >> 3, xc = tid & 7;
-    const uint32_t xoff = m0 + xrow < M ? (uint32_t)(m0 + xrow) * (uint32_t)K + (uint32_t)xc * 16u : kOob;
-    const int xlds = xrow * 128 + ((xc ^ ((xrow >> 1) & 7)) << 4);
-    // W: thread t stages chunks q = t + 512 j (tile row q / 8, chunk q % 8).
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
-    uint32_t woff[2];
-    int wlds[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int q = tid + 512 * j, row = q >> 3, c = q & 7;
-        woff[j] = n0 + row < N ? (uint32_t)(n0 + row) * (uint32_t)K + (uint32_t)c * 16u : kOob;
-        wlds[j] = kXS + row * 128 + ((c ^ ((row >> 1) & 7)) << 4);
-    }
-    // Scales: wave 0 lane r loads sx of tile row r (four blocks, 16 bytes); wave 1 lane u
-    // loads dw of block u / 16 of the stage, columns 8 (u % 16) .. + 7 (16 bytes); the
-    // block index is a per-lane offset (a buffer load's scalar offset is wave-uniform).
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(xs, (uint64_t)M * (uint64_t)nblk * 4u);
-    const __amdgpu_buffer_rsrc_t dr = make_rsrc(w.d, (uint64_t)N * (uint64_t)nblk * 2u);
-    const int dcol = 8 * (lane & 15), dblk = lane >> 4;
-    // the other waves' scale offsets are out of range: their loads move nothing
-    const uint32_t soff = wave == 0 && m0 + lane < M ? (uint32_t)(m0 + lane) * (uint32_t)nblk * 4u : kOob;
-    const uint32_t doff = wave == 1 && n0 + dcol < N ? ((uint32_t)dblk * (uint32_t)N + (uint32_t)(n0 + dcol)) * 2u : kOob;
-
-    struct Set {
-        u32x4 x, w[2], s, d;  // s: sx (wave 0 only), d: dw (wave 1 only)
-    };
-    Set set[R];
-    // Stage i covers blocks [4 i, 4 i + 4). The per-lane offsets are fixed and the stage
-    // enters as the scalar offset, so the loads carry no per-stage condition (a condition
-    // there became a branch, and the wait counts that the compiler derives across it waited
-    // for the first load of the same stage). Stages at or past ns take a scalar offset of
-    // 2^30: every offset is then either past the end of its buffer (the load returns zeros)
-    // or inside it. Bytes past K in a partial last stage come from the next row (or are past
-    // the end); no MFMA reads them.
-    auto load = [&](int i, Set &S_) {
-        const int kb0 = i * SB;
-        const bool live = i < ns;
-        const uint32_t kx = live ? (uint32_t)kb0 * 32u : 0x40000000u;
-        S_.x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff, kx, 0));
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-            S_.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], kx, 0));
-        S_.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, soff, live ? (uint32_t)kb0 * 4u : 0x40000000u, 0));
-        S_.d = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(dr, doff, live ? (uint32_t)kb0 * (uint32_t)N * 2u : 0x40000000u, 0));
-    };
-    auto store = [&](const Set &S_, int buf) {
-        uint8_t *const b = lds + buf * kBuf;
-        *reinterpret_cast<u32x4 *>(&b[xlds]) = S_.x;
-#pragma unroll
-        for (int j = 0; j < 2; j++) *reinterpret_cast<u32x4 *>(&b[wlds[j]]) = S_.w[j];
-        if (wave == 0) {
-            float *sx = reinterpret_cast<float *>(b + kXS + kWS) + lane;
-            const f32x4 v = __builtin_bit_cast(f32x4, S_.s);
-            sx[0 * BM] = v.x;
-            sx[1 * BM] = v.y;
-            sx[2 * BM] = v.z;
-            sx[3 * BM] = v.w;
-        } else if (wave == 1) {
-            float *dw = reinterpret_cast<float *>(b + kXS + kWS + kSxS) + dblk * BN + dcol;
-            // whole-vector casts only: this compiler's __builtin_bit_cast of one element of an
-            // ext_vector lvalue (v.y, v[i]) reads element 0
-            const f32x8 f = __builtin_convertvector(__builtin_bit_cast(f16x8, S_.d), f32x8);
-            *reinterpret_cast<f32x4 *>(dw) = __builtin_shufflevector(f, f, 0, 1, 2, 3);
-            *reinterpret_cast<f32x4 *>(dw + 4) = __builtin_shufflevector(f, f, 4, 5, 6, 7);
-        }
-    };
-    // Operand reads of block kb: A row 32 wm + lane % 32, B row 32 wn + lane % 32, chunk
-    // 2 kb + lane / 32 of the stage's 128 bytes.
-    const int ra = 32 * wm + l32, rb = 32 * wn + l32;
-    const int asw = (ra >> 1) & 7, bsw = (rb >> 1) & 7;
-    float acc[16];
-#pragma unroll
-    for (int v = 0; v < 16; v++) acc[v] = 0.f;
-    auto mfma = [&](const uint8_t *b, int kb) {
-        const int ch = 2 * kb + h;
-        const i32x4 a = *reinterpret_cast<const i32x4 *>(&b[ra * 128 + ((ch ^ asw) << 4)]);
-        const i32x4 q = *reinterpret_cast<const i32x4 *>(&b[kXS + rb * 128 + ((ch ^ bsw) << 4)]);
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i32x16{}, 0, 0, 0);
-    };
-    // Scale products of blocks 2 p and 2 p + 1 of the stage on the matrix core: lane
-    // (h, l32) supplies sx of row ra and dw of column rb for block 2 p + h, and
-    // v_mfma_f32_32x32x1_2b_f32 returns the two 32 x 32 outer products (block 2 p in
-    // elements 0..15, block 2 p + 1 in 16..31) in the layout of the int8 product. Each
-    // element is a0 * b0 + 0 rounded once: the fp32 product fl(sx * dw), bar the sign of a
-    // zero, which the fold below cannot see (its accumulator is never -0).
-    auto scales = [&](const uint8_t *b, int p) {
-        const float sx = reinterpret_cast<const float *>(b + kXS + kWS)[(2 * p + h) * BM + ra];
-        const float dw = reinterpret_cast<const float *>(b + kXS + kWS + kSxS)[(2 * p + h) * BN + rb];
-        return __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dw, f32x32{}, 0, 0, 0);
-    };
-    auto half = [](const f32x32 &P, int e) {
-        return e == 0 ? __builtin_shufflevector(P, P, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15)
-                      : __builtin_shufflevector(P, P, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
-    };
-    // result element v: row 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32
-    auto fold = [&](const i32x16 &I, const f32x16 &p) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], p[v], acc[v]);
-    };
-
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        load(r, set[r]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    store(set[0], 0);
-    // Iteration i: the barrier publishes stage i (stored during iteration i - 1) and frees
-    // the other buffer (its last reader, stage i - 1, is done); the loads of stage i + R go
-    // into the set stage i came from; stage i + 1 is stored while stage i is computed.
-    for (int i0 = 0; i0 < ns; i0 += R) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int i = i0 + r;  // i0 is a multiple of the even R: buffer i % 2 == r % 2
-            __syncthreads();
-            load(i + R, set[r]);
-            __builtin_amdgcn_sched_barrier(0);
-            store(set[(r + 1) % R], (r + 1) & 1);
-            const uint8_t *b = lds + (r & 1) * kBuf;
-            const int kb0 = i * SB;
-            if (kb0 + SB <= nblk) {
-                // the stage's products first: the matrix core runs them back to back while
-                // the vector ALU folds the earlier ones
-                i32x16 I[SB];
-                f32x32 P[SB / 2];
-#pragma unroll
-                for (int kb = 0; kb < SB; kb++) {
-                    I[kb] = mfma(b, kb);
-                    if (kb & 1) P[kb >> 1] = scales(b, kb >> 1);
-                }
-#pragma unroll
-                for (int kb = 0; kb < SB; kb++) fold(I[kb], half(P[kb >> 1], kb & 1));
-            } else {
-#pragma unroll
-                for (int p = 0; p < SB / 2; p++) {
-                    if (kb0 + 2 * p >= nblk) break;
-                    const f32x32 P = scales(b, p);
-#pragma unroll
-                    for (int e = 0; e < 2; e++)
-                        if (kb0 + 2 * p + e < nblk) fold(mfma(b, 2 * p + e), half(P, e));
-                }
-            }
-        }
-    }
-    const int col = n0 + rb;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int row = m0 + 32 * wm + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (row < M && col < N) y[(int64_t)row * N + col] = acc[v];
-    }
-}
+// quantized activations and the Q8_0 quants of block b; every output is folded by one lane
+// (over all of K, or over each of a few contiguous K ranges whose partials are then added in
+// order), so results are bit-identical to a sequential fp32 loop over the blocks (the
+// oracle's emulation). The scale products fl(sx * dw) come from the matrix core as outer
+// products in the int8 product's layout, so the vector ALU does two operations per output
+// and block (convert, FMA). Kernels: gemm_i8_small (M <= 256) and gemm_i8_lds (above).
 
 }  // namespace gw
 }  // namespace j4q
@@ -886,7 +698,7 @@ namespace gw {
 
 typedef int32_t i32x4s __attribute__((ext_vector_type(4)));
 
-// Prefill GEMM, int8 variant for small M: the fold of gemm_i8_wide on 16 x 32 tiles, with K
+// Prefill GEMM, int8 variant for small M: the fold above on 16 x 32 tiles, with K
 // cut into RG = 1 or 4 contiguous ranges of whole stages, each run by its own pair of waves
 // through its own LDS buffers. With one lane per output over all of K, M = 32 would have only
 // 512 16 x 16 tiles (two waves per CU) whose 32 stages run back to back; four ranges give
@@ -897,7 +709,8 @@ typedef int32_t i32x4s __attribute__((ext_vector_type(4)));
 // folded in block order into its partial; the partials meet at the end as
 // ((p0 + p1) + p2) + p3, the association of the oracle's emulation with four ranges.
 // Stages of four blocks (one 128-byte line per row) go through two LDS buffers per range
-// with the XOR swizzle of gemm_i8_wide; a stage's four MFMAs are issued before their folds.
+// with 16-byte chunk c of row r at chunk c ^ ((r / 2) % 8) of 128-byte rows (the 16 rows of an
+// operand read fall on distinct banks); a stage's four MFMAs are issued before their folds.
 // Every range runs the same number of iterations (its stages past its range load nothing
 // and compute nothing), so all waves meet at every barrier. Requires K % 32 == 0,
 // N % 8 == 0, M * K < 2^31 and N * K < 2^31.
@@ -956,9 +769,11 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
         u32x4 x, w[2], s, d;
     };
     Set set[R];
-    // Fixed per-lane offsets and the stage as the scalar offset, as in gemm_i8_wide: stages
-    // past the range take 2^30 (every offset then past the end of its buffer or inside
-    // it); bytes past K in the last stage are never read by an MFMA.
+    // Fixed per-lane offsets and the stage as the scalar offset, so the loads carry no
+    // per-stage condition (a condition there became a branch, and the wait counts the
+    // compiler derives across it waited for the first load of the same stage): stages past
+    // the range take 2^30 (every offset then past the end of its buffer or inside it); bytes
+    // past K in the last stage are never read by an MFMA.
     auto load = [&](int i, Set &S_) {
         const bool live = i < ns;
         const int kb0 = kbs + i * SB;
@@ -984,7 +799,8 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
             sx[3 * BM] = v.w;
         } else if (dthr) {
             float *dw = reinterpret_cast<float *>(b + kXS + kWS + kSxS) + dblk * BN + dcol;
-            // whole-vector casts only (see gemm_i8_wide)
+            // whole-vector casts only: this compiler's __builtin_bit_cast of one element of an
+            // ext_vector lvalue (v.y, v[i]) reads element 0
             const f32x8 f = __builtin_convertvector(__builtin_bit_cast(f16x8, S_.d), f32x8);
             *reinterpret_cast<f32x4 *>(dw) = __builtin_shufflevector(f, f, 0, 1, 2, 3);
             *reinterpret_cast<f32x4 *>(dw + 4) = __builtin_shufflevector(f, f, 4, 5, 6, 7);
@@ -1082,30 +898,33 @@ gemm_i8_small(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ x
 namespace j4q {
 namespace gw {
 
-// Prefill GEMM, int8 variant with the tiles loaded straight into LDS and the fold of each
-// block pair overlapped with the next pair's products: the same arithmetic as gemm_i8_wide
-// (every output folded by one lane over all of K in block order, fma(float(I_b),
-// fl(sx * dw), acc)), so results are bit-identical to it and to the oracle's emulation.
+// Prefill GEMM, int8 variant above M = 256, with the tiles loaded straight into LDS and the
+// fold of each block pair overlapped with the next pair's products (every output folded
+// by one lane over all of K in block order: bit-identical to the oracle's emulation).
 //  - Tile 64 x 128 per workgroup of 8 waves (two per SIMD); wave w owns the 32 x 32 outputs
-//    of rows 32 (w % 2), columns 32 (w / 2). K advances in stages of four blocks.
+//    of rows 32 (w % 2), columns 32 (w / 2). K advances in stages of four blocks (one 128-byte
+//    line of every row).
 //  - Every stage moves straight from global memory into one of three LDS stage buffers
-//    (buffer_load ... lds, no VGPRs, no LDS stores): X as 64 rows x 128 bytes and W as 128
-//    rows x 128 bytes (16-byte chunk c of row r at slot c ^ ((r / 2) % 8), so the rows of an
-//    operand read spread over the banks), then sx as [64 rows][4 blocks] fp32 and dw as
-//    [4 blocks][128 columns] fp16 (from the block-major copy). A lane loads the global chunk
-//    that belongs at its LDS slot. Every wave issues exactly four loads per stage (X, two W,
-//    a quarter of sx or of dw), so all waves wait for the same count and no load sits behind
-//    a branch.
-//  - Iteration i: wait for own stage-i loads, barrier, load stage i + 2 into the buffers of
-//    stage i - 1 (the ring's look-ahead past the end loads the last stage again), then per
-//    block pair: read its operands, issue its two int8 products and its scale-product MFMA,
-//    and fold the pair before it (still in registers) while the matrix core runs, so the
-//    vector-ALU work of one pair overlaps the matrix work of the next in every wave.
-// Requires K % 32 == 0, N % 8 == 0, M * K < 2^31 and N * K < 2^31.
-template <int SCHED>
-__global__ void __launch_bounds__(512)
+//    (buffer_load ... lds, no VGPRs, no LDS stores): X as 64 rows and W as 128 rows of 128
+//    bytes, 16-byte chunk c of row r at slot c ^ ((r / 2) % 8), so the 16 rows of one
+//    quarter-wave of an operand read cover all 64 banks; then sx as [64 rows][4 blocks] fp32
+//    and dw as [4 blocks][128 columns] fp16 (from the block-major copy). A lane loads the
+//    global chunk that belongs at its LDS slot. Every wave issues four loads per stage (X, two
+//    of W, a quarter of sx or of dw), so all waves wait for the same count and no load sits
+//    behind a branch.
+//  - Iteration i: wait for own stage-i loads, barrier, then stage i with the four loads of
+//    stage i + 2 (into the buffers of stage i - 1; the ring's look-ahead past the end loads
+//    the last stage again) between its steps. A stage reads a pair's operands a step before
+//    its MFMAs and folds the pair before it in between, so the LDS latency, the matrix work
+//    and the fold overlap in every wave (measured on MI355X at N = K = 4096, quantizer
+//    included: M = 512 36.8 us and M = 2048 136 us, against 43.8 and 159 us for the same tile
+//    loaded through registers and folded right after its own products; stages of eight blocks
+//    with half the barriers ran 39.7 us at M = 512).
+// Requires K % 32 == 0, N % 8 == 0, M * K < 2^31 and N * K < 2^31. Internal linkage: this header
+// is included by more than one source.
+[[maybe_unused]] static __global__ void __launch_bounds__(512)
 gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc, float *__restrict__ y, int M) {
-    constexpr int BM = 64, BN = 128, SB = 4;
+    constexpr int BM = 64, BN = 128, SB = 4;  // rows, columns, blocks per stage
     constexpr int kX = BM * 128, kW = BN * 128, kSx = BM * SB * 4, kS = kSx + SB * BN * 2;
     __shared__ __attribute__((aligned(1024))) uint8_t xs0[kX], xs1[kX], xs2[kX];
     __shared__ __attribute__((aligned(1024))) uint8_t ws0[kW], ws1[kW], ws2[kW];
@@ -1124,16 +943,15 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int wm = wave & 1, wn = wave >> 1, h = lane >> 5, l32 = lane & 31;
 
-    // X: wave w fills rows 8 w .. 8 w + 7 (lane L the slot L % 8 of row 8 w + L / 8); W:
-    // load j of wave w fills rows 8 (8 j + w) .. + 7.
+    // X: wave w fills rows 8 w .. 8 w + 7 (lane L the slot L % 8 of row 8 w + L / 8); W: load
+    // j of wave w fills rows 8 (8 j + w) .. + 7.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(xq, (uint64_t)M * (uint64_t)K);
-    uint32_t xoff;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
+    uint32_t xoff, woff[2];
     {
         const int row = 8 * wave + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
         xoff = m0 + row < M ? (uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)c * 16u : kOob;
     }
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w.qs, (uint64_t)N * (uint64_t)K);
-    uint32_t woff[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int row = 8 * (8 * j + wave) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
@@ -1157,14 +975,14 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
     }
     const uint32_t cstep = sxw ? 4u * SB : (uint32_t)N * 2u * SB;  // bytes per stage
 
-    // Loads of stage i (clamped to the last stage, which the ring's look-ahead past the end
-    // reads again: in range, never computed on).
-    auto load = [&](int i, uint8_t *xb, uint8_t *wb, uint8_t *sb) {
+    // Load j (0: X, 1 and 2: W, 3: scales) of stage i, clamped to the last stage (which the
+    // ring's look-ahead past the end reads again: in range, never computed on).
+    auto load = [&](int i, int j, uint8_t *xb, uint8_t *wb, uint8_t *sb) __attribute__((always_inline)) {
         const uint32_t st = (uint32_t)(i < ns ? i : ns - 1);
-        dma16(xr, xb + wave * 1024, xoff, st * (SB * 32u));
-        dma16(wr, wb + wave * 1024, woff[0], st * (SB * 32u));
-        dma16(wr, wb + (8 + wave) * 1024, woff[1], st * (SB * 32u));
-        dma4s(cr, sb + wave * 256, coff, st * cstep);
+        if (j == 0) dma16(xr, xb + wave * 1024, xoff, st * 128u);
+        else if (j == 1) dma16(wr, wb + wave * 1024, woff[0], st * 128u);
+        else if (j == 2) dma16(wr, wb + (8 + wave) * 1024, woff[1], st * 128u);
+        else dma4s(cr, sb + wave * 256, coff, st * cstep);
     };
 
     const int ra = 32 * wm + l32, rb = 32 * wn + l32;
@@ -1173,58 +991,90 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[v] = 0.f;
     // result element v: row 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32
-    auto fold = [&](const i32x16 &I, const f32x32 &P, int e) {
+    auto fold = [&](const i32x16 &I, const f32x32 &Pr, int e) __attribute__((always_inline)) {
 #pragma unroll
-        for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], P[16 * e + v], acc[v]);
+        for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)I[v], Pr[16 * e + v], acc[v]);
     };
-    // products of block pair p of a stage (blocks 2 p, 2 p + 1) and their scale products:
-    // lane (h, l32) supplies sx of row ra and dw of column rb for block 2 p + h, and
-    // v_mfma_f32_32x32x1_2b_f32 returns both 32 x 32 outer products (block 2 p in elements
-    // 0..15, 2 p + 1 in 16..31) in the layout of the int8 products
     struct Pair {
         i32x16 I0, I1;
-        f32x32 P;
+        f32x32 Pr;
     };
-    auto products = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *sb, int p, Pair &out) {
-        const int c0 = 4 * p + h, c1 = 4 * p + 2 + h;  // chunks of blocks 2 p and 2 p + 1
-        const i32x4 a0 = *reinterpret_cast<const i32x4 *>(xb + ra * 128 + ((c0 ^ asw) << 4));
-        const i32x4 b0 = *reinterpret_cast<const i32x4 *>(wb + rb * 128 + ((c0 ^ bsw) << 4));
-        const i32x4 a1 = *reinterpret_cast<const i32x4 *>(xb + ra * 128 + ((c1 ^ asw) << 4));
-        const i32x4 b1 = *reinterpret_cast<const i32x4 *>(wb + rb * 128 + ((c1 ^ bsw) << 4));
-        const float sx = reinterpret_cast<const float *>(sb)[ra * SB + 2 * p + h];
-        const float dw = half_bits_to_float(reinterpret_cast<const uint16_t *>(sb + kSx)[(2 * p + h) * BN + rb]);
-        out.I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, i32x16{}, 0, 0, 0);
-        out.I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, i32x16{}, 0, 0, 0);
-        out.P = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dw, f32x32{}, 0, 0, 0);
+    // operands of block pair p of a stage (blocks 2 p and 2 p + 1: chunks c0 and c1 of the
+    // row's line)
+    struct Ops {
+        i32x4 a0, b0, a1, b1;
+        float sx, dw;
     };
-    // prev: the pair still to be folded; zeros before the first stage, whose fold adds exact
-    // zeros (fma(0, 0, +0) = +0)
-    Pair prev, cur;
-    prev.I0 = i32x16{};
-    prev.I1 = i32x16{};
-    prev.P = f32x32{};
-    // One full stage: pair 0's products with the fold of the pair before, then pair 1's
-    // products with the fold of pair 0; pair 1 stays pending for the next stage.
-    auto stage = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *sb) {
-        products(xb, wb, sb, 0, cur);
-        fold(prev.I0, prev.P, 0);
-        fold(prev.I1, prev.P, 1);
+    auto read_ops = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *sb, int p, Ops &o) __attribute__((always_inline)) {
+        const int c0 = 4 * p + h, c1 = 4 * p + 2 + h;
+        o.a0 = *reinterpret_cast<const i32x4 *>(xb + ra * 128 + ((c0 ^ asw) << 4));
+        o.b0 = *reinterpret_cast<const i32x4 *>(wb + rb * 128 + ((c0 ^ bsw) << 4));
+        o.a1 = *reinterpret_cast<const i32x4 *>(xb + ra * 128 + ((c1 ^ asw) << 4));
+        o.b1 = *reinterpret_cast<const i32x4 *>(wb + rb * 128 + ((c1 ^ bsw) << 4));
+        o.sx = reinterpret_cast<const float *>(sb)[ra * SB + 2 * p + h];
+        o.dw = half_bits_to_float(reinterpret_cast<const uint16_t *>(sb + kSx)[(2 * p + h) * BN + rb]);
+    };
+    // the pair's int8 products and scale products: lane (h, l32) supplies sx of row ra and
+    // dw of column rb for block 2 p + h, and v_mfma_f32_32x32x1_2b_f32 returns both 32 x 32
+    // outer products (block 2 p in elements 0..15, 2 p + 1 in 16..31) in the layout of the
+    // int8 products
+    auto products = [&](const Ops &o, Pair &out) __attribute__((always_inline)) {
+        out.I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a0, o.b0, i32x16{}, 0, 0, 0);
+        out.I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a1, o.b1, i32x16{}, 0, 0, 0);
+        out.Pr = __builtin_amdgcn_mfma_f32_32x32x1f32(o.sx, o.dw, f32x32{}, 0, 0, 0);
+    };
+    // pa: pair 0 of the current stage; pb: the pair left for folding (pair 1 of the stage
+    // before; zeros before the first stage, whose fold adds exact zeros: fma(0, 0, +0) = +0)
+    Pair pa, pb;
+    pb.I0 = i32x16{};
+    pb.I1 = i32x16{};
+    pb.Pr = f32x32{};
+    // One stage, each step fenced from the next: read pair 0's operands, fold block 0 of the
+    // left pair (its latency covers the reads), pair 0's products, read pair 1's operands,
+    // fold block 1 of the left pair, pair 1's products, then fold pair 0 while pair 1's
+    // products run; pair 1 is left for the next stage. The four loads of stage i + 2 sit
+    // between the steps, so a wave never issues them back to back. (Every lambda here is
+    // forced inline: the five calls of step were otherwise kept as calls, with a stack frame
+    // in scratch memory.)
+    auto stage = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *sb, int inext, uint8_t *xn, uint8_t *wn,
+                     uint8_t *sn) __attribute__((always_inline)) {
+        Ops o;
+        read_ops(xb, wb, sb, 0, o);
         __builtin_amdgcn_sched_barrier(0);
-        products(xb, wb, sb, 1, prev);
-        fold(cur.I0, cur.P, 0);
-        fold(cur.I1, cur.P, 1);
+        load(inext, 0, xn, wn, sn);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(pb.I0, pb.Pr, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        products(o, pa);
+        __builtin_amdgcn_sched_barrier(0);
+        read_ops(xb, wb, sb, 1, o);
+        __builtin_amdgcn_sched_barrier(0);
+        load(inext, 1, xn, wn, sn);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(pb.I1, pb.Pr, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load(inext, 2, xn, wn, sn);
+        __builtin_amdgcn_sched_barrier(0);
+        products(o, pb);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(pa.I0, pa.Pr, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(inext, 3, xn, wn, sn);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(pa.I1, pa.Pr, 1);
         __builtin_amdgcn_sched_barrier(0);
     };
     auto step = [&](int i, const uint8_t *xb, const uint8_t *wb, const uint8_t *sb, uint8_t *xn, uint8_t *wn,
-                    uint8_t *sn) {
+                    uint8_t *sn) __attribute__((always_inline)) {
         wait_vm_lgkm0<4>();
         lds_barrier();
-        load(i + 2, xn, wn, sn);
-        stage(xb, wb, sb);
+        stage(xb, wb, sb, i + 2, xn, wn, sn);
     };
 
-    load(0, xs0, ws0, ss0);
-    load(1, xs1, ws1, ss1);
+#pragma unroll
+    for (int j = 0; j < 4; j++) load(0, j, xs0, ws0, ss0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) load(1, j, xs1, ws1, ss1);
     int i = 0;
     for (; i + 3 <= nfull; i += 3) {
         step(i, xs0, ws0, ss0, xs2, ws2, ss2);
@@ -1239,8 +1089,8 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
             i++;
         }
     }
-    fold(prev.I0, prev.P, 0);
-    fold(prev.I1, prev.P, 1);
+    fold(pb.I0, pb.Pr, 0);
+    fold(pb.I1, pb.Pr, 1);
     // a last stage of 1..3 blocks (in buffer i % 3)
     if (nfull < ns) {
         const int r = i % 3;
@@ -1251,9 +1101,11 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
         lds_barrier();
         const int nb = nblk - nfull * SB;
         for (int p = 0; 2 * p < nb; p++) {
-            products(xb, wb, sb, p, cur);
-            fold(cur.I0, cur.P, 0);
-            if (2 * p + 1 < nb) fold(cur.I1, cur.P, 1);
+            Ops o;
+            read_ops(xb, wb, sb, p, o);
+            products(o, pa);
+            fold(pa.I0, pa.Pr, 0);
+            if (2 * p + 1 < nb) fold(pa.I1, pa.Pr, 1);
         }
     }
     const int col = n0 + rb;
