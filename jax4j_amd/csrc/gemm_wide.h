@@ -420,9 +420,16 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
 #pragma unroll
             for (int p = 0; p < P; p++) load(inext, p, xn, wn, dn);
         }
+        // Operands of the stage's two blocks (bb = 0, 1). Block 0's W is dequantized before
+        // its MFMAs; block 1's operands are read right behind it, and its W is dequantized
+        // between block 0's MFMAs, so the vector ALU work of one block overlaps the matrix
+        // work of the other (all at once before the MFMAs, the two waves of a SIMD dequantized
+        // in step and left the matrix core idle meanwhile). The MFMAs of every accumulator run
+        // in the same order as before, so results do not change.
         bf16x8 a[2][TM], b[2][NJ];
-#pragma unroll
-        for (int bb = 0; bb < 2; bb++) {
+        u32x2 q1[NJ];
+        uint32_t d1[NJ];
+        auto read_block = [&](int bb, u32x2 (&q)[NJ], uint32_t (&d)[NJ]) {
             const int ca = 4 * (2 * bb + kh) + g;
             const int aoff = m16 * 256 + ((ca ^ m16) << 4);
 #pragma unroll
@@ -430,12 +437,21 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const int row = 16 * NJ * nw + 16 * j + m16, cb = 2 * (2 * bb + kh) + (g >> 1);
-                const u32x2 q = *reinterpret_cast<const u32x2 *>(wb + row * 128 + ((cb ^ wswz(row)) << 4) + 8 * (g & 1));
-                const uint32_t dbits = *reinterpret_cast<const uint16_t *>(db + wave * 256 + (bb * 16 * NJ + 16 * j + m16) * 2);
-                b[bb][j] = dequant8(q, half_bits_to_float(dbits));
+                q[j] = *reinterpret_cast<const u32x2 *>(wb + row * 128 + ((cb ^ wswz(row)) << 4) + 8 * (g & 1));
+                d[j] = *reinterpret_cast<const uint16_t *>(db + wave * 256 + (bb * 16 * NJ + 16 * j + m16) * 2);
             }
+        };
+        {
+            u32x2 q0[NJ];
+            uint32_t d0[NJ];
+            read_block(0, q0, d0);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) b[0][j] = dequant8(q0[j], half_bits_to_float(d0[j]));
         }
+        read_block(1, q1, d1);
         constexpr int NM = 2 * TM * NJ, STRIDE = NM / P > 0 ? NM / P : 1;
+        // block 1's column tile j is dequantized after block 0's MFMA number DQ (j + 1) - 1
+        constexpr int DQ = TM * NJ / (NJ + 1) > 0 ? TM * NJ / (NJ + 1) : 1;
         int mi = 0, p = 0;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++)
@@ -449,6 +465,10 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
                         load(inext, p, xn, wn, dn);
                         __builtin_amdgcn_sched_barrier(0);
                         p++;
+                    }
+                    if (bb == 0 && (mi + 1) % DQ == 0 && (mi + 1) / DQ <= NJ) {
+                        const int jj = (mi + 1) / DQ - 1;
+                        b[1][jj] = dequant8(q1[jj], half_bits_to_float(d1[jj]));
                     }
                     mi++;
                 }
