@@ -389,8 +389,15 @@ int check_gemm_weights(const Buf &w, int variant, const char *op) {
 
 // Takes the weight type by value: callers read it before alloc_buf, whose registration of the
 // output can move the buffer table (and every Buf pointer into it).
-hipError_t launch_gemm_bf16(int qtype, const j4q::QMat &m, const uint16_t *x, float *y, int64_t rows, hipStream_t s) {
-    return qtype == J4Q_Q8_0 ? j4q::launch_gemm_q8_bf16(m, x, y, rows, s) : j4q::launch_gemm_kq_bf16(qtype, m, x, y, rows, s);
+hipError_t launch_gemm_bf16(int qtype, const j4q::QMat &m, const uint16_t *x, float *y, int64_t rows, float *ws,
+                            hipStream_t s) {
+    return qtype == J4Q_Q8_0 ? j4q::launch_gemm_q8_bf16(m, x, y, rows, s) : j4q::launch_gemm_kq_bf16(qtype, m, x, y, rows, ws, s);
+}
+
+// Workspace of a bf16 GEMM (the K-quant kernels' split partials; none for Q8_0), at most
+// 32 MiB.
+uint64_t gemm_bf16_workspace(int qtype, const j4q::QMat &m, int64_t rows) {
+    return qtype == J4Q_Q8_0 ? 0 : j4q::gemm_kq_workspace_bytes(qtype, m, rows);
 }
 
 }  // namespace
@@ -798,7 +805,12 @@ int j4q_quant_matmul(j4q_buffer wh, j4q_buffer xh, int variant, j4q_buffer *out)
     void *ydev;
     if ((rc = alloc_buf(J4Q_KIND_F32, 2, M, N, (uint64_t)(M * N) * 4, out, &ydev))) return rc;
     if (variant == J4Q_GEMM_BF16) {
-        LAUNCH_INTO("quantMatmul", out, launch_gemm_bf16(qt, m, xdev, (float *)ydev, M, g_stream));
+        void *ws = nullptr;
+        const uint64_t wsb = gemm_bf16_workspace(qt, m, M);
+        if (wsb) LAUNCH_INTO("hipMallocAsync", out, hipMallocAsync(&ws, wsb, g_stream));
+        const hipError_t e = launch_gemm_bf16(qt, m, xdev, (float *)ydev, M, (float *)ws, g_stream);
+        if (ws) (void)hipFreeAsync(ws, g_stream);
+        LAUNCH_INTO("quantMatmul", out, e);
         return J4Q_OK;
     }
     void *ws = nullptr;
@@ -866,7 +878,12 @@ int j4q_quant_matmul_into(j4q_buffer wh, const uint16_t *x, int64_t m, int varia
     const hipStream_t s = pick_stream(stream);
     const j4q::QMat mm = qmat_of(*w);
     if (variant == J4Q_GEMM_BF16) {
-        HIP_TRY("quantMatmul_into", launch_gemm_bf16(w->qtype, mm, x, y, m, s));
+        void *ws = nullptr;
+        const uint64_t wsb = gemm_bf16_workspace(w->qtype, mm, m);
+        if (wsb) HIP_TRY("hipMallocAsync", hipMallocAsync(&ws, wsb, s));
+        const hipError_t e = launch_gemm_bf16(w->qtype, mm, x, y, m, (float *)ws, s);
+        if (ws) (void)hipFreeAsync(ws, s);
+        HIP_TRY("quantMatmul_into", e);
         return J4Q_OK;
     }
     HIP_TRY("quantMatmul_into", j4q::launch_quantize_act(x, m, mm.cols, xq, xs, s));
@@ -895,7 +912,9 @@ int j4q_quant_matmul_noalloc(j4q_buffer wh, const uint16_t *x, int64_t m, int va
     const hipStream_t s = pick_stream(stream);
     const j4q::QMat mm = qmat_of(*w);
     if (variant == J4Q_GEMM_BF16) {
-        HIP_TRY("quantMatmul_noalloc", launch_gemm_bf16(w->qtype, mm, x, y, m, s));
+        // the K-quant kernels' split partials (at most 32 MiB) go to the engine's array
+        static_assert(kScratchBytes >= (32ull << 20), "scratch holds the bf16 GEMM's workspace");
+        HIP_TRY("quantMatmul_noalloc", launch_gemm_bf16(w->qtype, mm, x, y, m, (float *)g_scratch, s));
         return J4Q_OK;
     }
     int8_t *xq = (int8_t *)g_scratch;

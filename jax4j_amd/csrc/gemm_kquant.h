@@ -27,8 +27,10 @@
 //  - Iteration i: wait for own stage-i loads, barrier, load stage i + 2 into the buffers of
 //    stage i - 1, read the operands of stage i, dequantize, run the MFMAs. Stages past the
 //    end load zeros (out-of-range offsets: zero quants and zero scales decode to 0).
-// grid = ceil(M / BM) * ceil(N / (64 NJ)) workgroups of 512 threads. Requires K % 128 == 0
-// (K % 256 for the K-quants), M * K * 2 < 2^31 and N * K / 2 < 2^31.
+// grid = (ceil(M / BM) * ceil(N / (64 NJ)), S) workgroups of 512 threads: S K splits of
+// split_stages stages each (S = 1: the whole of K, written to y; S > 1: partial tiles to
+// part[s][M][N], added by sum_splits_kernel). Requires K % 128 == 0 (K % 256 for the
+// K-quants), M * K * 2 < 2^31 and N * K / 2 < 2^31.
 #pragma once
 
 #include "gemm_wide.h"
@@ -101,14 +103,20 @@ struct KqTile {
 
 template <int FMT, int BM, int NJ>
 __global__ void __launch_bounds__(512)
-gemm_kq_bf16(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M) {
+gemm_kq_bf16(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int M, int split_stages,
+             float *__restrict__ part) {
     using T = KqTile<FMT, BM, NJ>;
     constexpr int BN = T::BN, TM = T::TM, XD = T::XD, RW = T::RW, QHL = T::QHL, P = T::P;
     __shared__ __attribute__((aligned(1024))) uint8_t xs0[T::kX], xs1[T::kX], xs2[T::kX];
     __shared__ __attribute__((aligned(1024))) uint8_t qs0[T::kQ], qs1[T::kQ], qs2[T::kQ];
     __shared__ __attribute__((aligned(256))) uint8_t hs0[T::kH], hs1[T::kH], hs2[T::kH];
     __shared__ __attribute__((aligned(256))) uint8_t ss0[T::kS], ss1[T::kS], ss2[T::kS];
-    const int N = (int)w.rows, K = (int)w.cols, ns = K / 128;
+    const int N = (int)w.rows, K = (int)w.cols;
+    // K split: workgroup (tile, s) takes stages [s L, min((s + 1) L, K / 128)) (L =
+    // split_stages) and writes its partial tile to part[s] when part is set (the splits are
+    // added in order by sum_splits_kernel), else the tile itself to y
+    const int sbeg = (int)blockIdx.y * split_stages, send0 = sbeg + split_stages;
+    const int ns = send0 < K / 128 ? send0 : K / 128;  // stages at or past ns load nothing
     const int mt = (M + BM - 1) / BM;
     // Workgroup b runs on XCD b % 8; tile order is m fastest and each XCD takes a contiguous
     // range of it, so the m tiles of a group of n tiles (the same W rows) share an L2.
@@ -278,10 +286,10 @@ gemm_kq_bf16(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int 
     };
 
 #pragma unroll
-    for (int p = 0; p < P; p++) load(0, p, xs0, qs0, hs0, ss0);
+    for (int p = 0; p < P; p++) load(sbeg, p, xs0, qs0, hs0, ss0);
 #pragma unroll
-    for (int p = 0; p < P; p++) load(1, p, xs1, qs1, hs1, ss1);
-    for (int i0 = 0; i0 < ns; i0 += 3) {
+    for (int p = 0; p < P; p++) load(sbeg + 1, p, xs1, qs1, hs1, ss1);
+    for (int i0 = sbeg; i0 < ns; i0 += 3) {
         wait_vm_lgkm0<P>();
         lds_barrier();
         stage(xs0, qs0, hs0, ss0, i0, xs2, qs2, hs2, ss2);
@@ -298,6 +306,7 @@ gemm_kq_bf16(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int 
     // 16 t + 4 g + v, column 16 j + lane % 16 of the wave's columns.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    float *const out = part ? part + (int64_t)blockIdx.y * M * N : y;
     float *red = reinterpret_cast<float *>(nw < 2 ? xs0 : xs1);
     if (kh == 1) {
 #pragma unroll
@@ -317,8 +326,29 @@ gemm_kq_bf16(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int 
             for (int v = 0; v < 4; v++) {
                 const int row = m0 + 16 * t + 4 * g + v, col = n0 + 16 * NJ * nw + 16 * j + m16;
                 const float s = acc[t][j][v] + red[((((nw & 1) * TM + t) * NJ + j) * 4 + v) * 64 + lane];
-                if (row < M && col < N) y[(int64_t)row * N + col] = s;
+                if (row < M && col < N) out[(int64_t)row * N + col] = s;
             }
+}
+
+// y[i] = ((part[0][i] + part[1][i]) + ...) for i < n: the K splits' partial products added
+// in split order (deterministic). A thread takes four consecutive elements when n % 4 == 0
+// (every split then starts 16-byte aligned; y is), else one.
+__global__ void __launch_bounds__(256)
+sum_splits_kernel(const float *__restrict__ part, int splits, int64_t n, float *__restrict__ y) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    if (n % 4 == 0) {
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n / 4; i += stride) {
+            f32x4 v = reinterpret_cast<const f32x4 *>(part)[i];
+            for (int r = 1; r < splits; r++) v += reinterpret_cast<const f32x4 *>(part + (int64_t)r * n)[i];
+            reinterpret_cast<f32x4 *>(y)[i] = v;
+        }
+        return;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+        float v = part[i];
+        for (int r = 1; r < splits; r++) v += part[(int64_t)r * n + i];
+        y[i] = v;
+    }
 }
 
 }  // namespace gk

@@ -145,7 +145,9 @@ hipError_t launch_gemm_q8_int8(const QMat &w, const int8_t *xq, const float *xs,
 hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s);
 // Prefill GEMM, bf16 variant, over Q4_0 (cols % 128 == 0), Q4_K and Q6_K weights.
 bool gemm_kq_supported(int id, int64_t cols);
-hipError_t launch_gemm_kq_bf16(int id, const QMat &w, const uint16_t *x, float *y, int64_t m, hipStream_t s);
+// Workspace the call needs (bytes; 0: none): the partial products of its K splits.
+uint64_t gemm_kq_workspace_bytes(int id, const QMat &w, int64_t m);
+hipError_t launch_gemm_kq_bf16(int id, const QMat &w, const uint16_t *x, float *y, int64_t m, float *ws, hipStream_t s);
 hipError_t launch_synth_quant(int id, uint64_t seed, int64_t rows, int64_t cols, uint8_t *gguf,
                               hipStream_t s);
 hipError_t launch_synth_f32(uint64_t seed, int64_t n, float *out, hipStream_t s);

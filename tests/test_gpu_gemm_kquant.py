@@ -146,12 +146,19 @@ def test_gemm_kquant_one_hot_rows_return_bf16_weights(backend, qt):
         backend.release(h)
 
 
+# (70, 160, 512): one K range; (20, 96, 4096): 32-row tiles and K in 8 ranges; (45, 130,
+# 2048): 64-row tiles, K in 4 ranges, and an output of M * N % 4 != 0 (the range sums take
+# one element per thread)
 @pytest.mark.parametrize("qt", KQ, ids=lambda q: q.name)
-def test_gemm_kquant_into_and_noalloc_match(backend, qt):
-    m, n, k = 70, 160, 512
+@pytest.mark.parametrize("m,n,k", [(70, 160, 512), (20, 96, 4096), (45, 130, 2048)])
+def test_gemm_kquant_into_and_noalloc_match(backend, qt, m, n, k):
+    """The three entry points agree bit for bit, also where K is split over workgroups (the
+    partial products then go through stream-ordered memory, or the engine's fixed array in
+    the allocation-free call, and are added in range order), and match the oracle."""
     note("gemm kquant into / noalloc", qt.name, m, n, k)
-    w_blob, xb, w, x = upload_case(backend, qt, m, n, k, 88)
+    w_blob, xb, w, x = upload_case(backend, qt, m, n, k, 88 + m)
     y_ref = backend.download(backend.quant_matmul(w, x, "bf16")).reshape(m, n)
+    check_rows(y_ref, xb, w_blob, qt, m, n, k)
     lib = N.load()
     ptr = lambda h: backend.buffer_desc(h).device_ptr
     for fn in ("into", "noalloc"):
