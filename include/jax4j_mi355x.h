@@ -183,7 +183,10 @@ int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *a
                           int64_t batch, void *stream);
 /* Prefill GEMM into caller memory (the weight types and variants of j4q_quant_matmul).
  * x_dev bf16 [m, cols]; y_dev fp32 [m, rows]. The int8 variant also needs xq_dev int8
- * [m, cols] and xs_dev fp32 [m, cols/32] as workspace; the bf16 variant ignores them. */
+ * [m, cols] and xs_dev fp32 [m, cols/32] as workspace; the bf16 variant ignores them. On
+ * Q4_0, Q4_K and Q6_K weights with a small grid (few rows of X) the bf16 variant splits K
+ * over workgroups and keeps the partial products in stream-ordered memory of `stream`
+ * (hipMallocAsync / hipFreeAsync, at most 32 MiB); nothing else is allocated. */
 int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, int8_t *xq_dev,
                           float *xs_dev, float *y_dev, void *stream);
 
@@ -193,9 +196,10 @@ int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, 
  * workspace (the quantized activations and their block scales) lives in one fixed engine
  * array of 36 MiB per GPU, so the call allocates nothing: x_dev bf16 [m, cols], y_dev fp32
  * [m, rows], both 16-byte aligned. The int8 variant needs m * cols <= 33554432 (32 MiB of
- * int8 activations, e.g. m = 8192 at cols = 4096), else J4Q_EUNSUPPORTED; the bf16 variant
- * has no workspace. Every call on a GPU shares that GPU's workspace: calls that overlap on
- * one GPU (on different streams, or from threads that do not order them) race. */
+ * int8 activations, e.g. m = 8192 at cols = 4096), else J4Q_EUNSUPPORTED. The bf16 variant
+ * over Q4_0, Q4_K and Q6_K keeps the partial products of its K split (at most 32 MiB) in the
+ * same array. Every call on a GPU shares that GPU's workspace: calls that overlap on one GPU
+ * (on different streams, or from threads that do not order them) race. */
 int j4q_quant_matmul_noalloc(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, float *y_dev,
                              void *stream);
 
