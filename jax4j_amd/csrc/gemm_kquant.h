@@ -265,6 +265,10 @@ gemm_kq_bf16(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int 
                      uint8_t *qn, uint8_t *hn, uint8_t *sn) {
 #pragma unroll
         for (int p = 0; p < P; p++) load(i + 2, p, xn, qn, hn, sn);
+        // Block 0's W is dequantized before its MFMAs, block 1's between them, so the vector
+        // ALU work of one block overlaps the matrix work of the other (both before the MFMAs,
+        // the two waves of a SIMD dequantized in step with the matrix core idle). Every
+        // accumulator's MFMAs keep their order, so results do not change.
         bf16x8 a[2][TM], b[2][NJ];
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
@@ -273,16 +277,25 @@ gemm_kq_bf16(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int 
             const int aoff = m16 * 256 + ((ca ^ m16) << 4);
 #pragma unroll
             for (int t = 0; t < TM; t++) a[bb][t] = *reinterpret_cast<const bf16x8 *>(xb + t * 16 * 256 + aoff);
-#pragma unroll
-            for (int j = 0; j < NJ; j++) b[bb][j] = bop(qb, hb, sb, i, c, j);
         }
+#pragma unroll
+        for (int j = 0; j < NJ; j++) b[0][j] = bop(qb, hb, sb, i, kh, j);
+        // block 1's column tile j is dequantized after block 0's MFMA number DQ (j + 1) - 1
+        constexpr int DQ = TM * NJ / (NJ + 1) > 0 ? TM * NJ / (NJ + 1) : 1;
+        int mi = 0;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++)
 #pragma unroll
             for (int t = 0; t < TM; t++)
 #pragma unroll
-                for (int j = 0; j < NJ; j++)
+                for (int j = 0; j < NJ; j++) {
                     acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[bb][t], b[bb][j], acc[t][j], 0, 0, 0);
+                    if (bb == 0 && (mi + 1) % DQ == 0 && (mi + 1) / DQ <= NJ) {
+                        const int jj = (mi + 1) / DQ - 1;
+                        b[1][jj] = bop(qb, hb, sb, i, 2 + kh, jj);
+                    }
+                    mi++;
+                }
     };
 
 #pragma unroll
