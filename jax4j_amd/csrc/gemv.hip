@@ -69,13 +69,16 @@ int g_cus = 256;
 //    the items per wave, twice the waves to hide the load latency: Q8_0 4096 x 4096 at B = 8
 //    12.8 -> 10.9 us, Q4_0 11008 x 4096 12.4 -> 12.0 us; Q4_K was 2 % slower and Q6_K spilled
 //    registers), else 8;
-//  - 9..16 rows: 4 waves of 8 blocks, windows of 32 blocks (1024 columns, a 64 KB x image,
-//    two workgroups per CU). Measured on the B = 16 decode step (all windows of a matrix in
-//    one launch): 3.41 ms at 4 waves, 3.42 ms at 8 (2048-column windows), where a CU holds
-//    8 waves either way; 8 waves of 4 blocks over the same 1024-column windows (16 waves per
-//    CU) took 3.02 ms against 2.69 ms for 4 waves of 8.
+//  - 9..16 rows: 8 waves of 8 blocks, windows of 64 blocks (2048 columns, a 128 KB x image
+//    and ~152-156 KB of LDS in all, one workgroup per CU): half the windows of 4 waves over
+//    1024 columns (two workgroups per CU), so half the partial sums for sum_windows_kernel
+//    to add, with the same 8 waves per CU. Measured on the B = 16 decode step (A/B on one
+//    box, all windows of a matrix in one launch): 2.29-2.31 ms against 2.43-2.46 ms for 4
+//    waves (the two were level, 3.42 against 3.41 ms, before the tile loop's wait-count
+//    fixes); 8 waves of 4 blocks over 1024-column windows (16 waves per CU) took 3.02 ms
+//    against 2.69 ms for 4 waves of 8.
 template <int FMT, int BB>
-constexpr int mfma_waves() { return BB > 8 ? 4 : (FMT == Q8_0 || FMT == Q4_0) ? 16 : 8; }
+constexpr int mfma_waves() { return BB > 8 ? 8 : (FMT == Q8_0 || FMT == Q4_0) ? 16 : 8; }
 template <int FMT, int BB>
 constexpr int mfma_ipw() { return BB > 8 ? (FMT == Q8_0 ? 4 : 2) : (FMT == Q8_0 ? 8 : 4) * 8 / mfma_waves<FMT, BB>(); }
 // Tiles in flight per wave: two (measured on the B = 16 decode step: 3.37 ms at 2, 3.52 ms

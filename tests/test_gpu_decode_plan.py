@@ -8,7 +8,7 @@ as the single calls, so its outputs equal the eager composition bit for bit; aga
 fp64 oracle chain the fp32 residual stream adds its roundings, bound 1e-4 * ||ref||_inf
 (10x inside the 1e-3 decode tolerance).
 
-A second, wider model gives every batched GEMV several column windows (K above 1024 columns
+A second, wider model gives every batched GEMV several column windows (K above 2048 columns
 at 9-16 batch rows, above 4096 at 3-8, all four formats), whose sums meet in a second launch
 on the plan's own workspace in the plan and on stream-ordered memory in the single calls:
 the two agree bit for bit, on every replay (the workspace is reused by every GEMV of a step).
@@ -39,9 +39,9 @@ class Dims:
 
 
 SMALL = Dims(512, 512, 256, 1024, 1000)
-# every batched GEMV over several column windows: K = 1536 (q|k|v, gate|up, head) and 4352
-# (down) have 2 and 5 windows at 16 rows, down 2 at 3-8 rows
-WIDE = Dims(1536, 1536, 512, 4352, 1000)
+# every batched GEMV over several column windows: K = 2560 (q|k|v, o, gate|up, head) and 4352
+# (down) have 2 and 3 windows at 16 rows, down 2 at 3-8 rows
+WIDE = Dims(2560, 2560, 512, 4352, 1000)
 # layer 0: one type per group (q|k|v and gate|up fused into one launch each); layer 1: v and
 # up of other types (runs launched separately, outputs copied into the fused layout)
 TYPES = [
