@@ -32,6 +32,10 @@ HIP_FLAGS = [
     # allocator rotated them through copies that each waited for the MFMA before, which
     # serialized the matrix pipe (19 instead of 44 cycles per 16x16x32 MFMA, measured)
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # the one atomic (a single lane's LDS add handing out row groups in the batch-1 GEMV) as a
+    # plain ds_add_rtn: the atomic optimizer's lane-count rewrite waited for its result and
+    # broadcast it right away, where the kernel reads it a group's worth of items later
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]

@@ -32,7 +32,9 @@ namespace {
 // workgroup of 16 waves per CU (every CU stages x once, at the start: with two workgroups
 // per CU the second one's x loads queued behind the first one's weight stream; the
 // Llama-3-8B decode step 1.226-1.232 -> 1.213-1.219 ms in an A/B on one box, the fused
-// gate|up and the output head taking it; 16 waves in two workgroups per CU had won
+// gate|up and the output head taking it), its waves taking row groups from the workgroup's
+// pool (gemv_kernel DYN: the fused gate|up 14.9-15.0 -> 13.7 us, the step 1.21-1.23 ->
+// 1.16-1.17 ms in an A/B on one box; 16 waves in two workgroups per CU had won
 // 1.271 -> 1.260 ms over 8-wave workgroups; a ring of 3 or 4 register sets at one workgroup
 // per CU lost, 1.25 and 1.28 ms; q|k|v at 16 waves lost, 6.3 -> 7.1 us); for K <= 8192, 2
 // workgroups per CU; for larger windows (an x image of up to 139 KB), 16 waves in one
@@ -42,7 +44,7 @@ template <int FMT>
 hipError_t launch_window(const QMat &m, const float *x, const float *prev, const float *add, float *y, int batch,
                          int cus, int64_t c0, int64_t kw, hipStream_t s) {
     if (kw <= 4096)
-        return m.rows >= 16384 ? gemv::launch<FMT, 1, 16, 2>(m, x, prev, add, y, batch, cus, c0, kw, s)
+        return m.rows >= 16384 ? gemv::launch<FMT, 1, 16, 2, true>(m, x, prev, add, y, batch, cus, c0, kw, s)
                                : gemv::launch<FMT, 1, 8, 2>(m, x, prev, add, y, batch, 2 * cus, c0, kw, s);
     if (kw <= 8192) return gemv::launch<FMT, 1, 8, 2>(m, x, prev, add, y, batch, 2 * cus, c0, kw, s);
     return gemv::launch<FMT, 1, 16, 2>(m, x, prev, add, y, batch, cus, c0, kw, s);

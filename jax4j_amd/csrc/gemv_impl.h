@@ -385,11 +385,19 @@ struct TraceSink {
 };
 extern TraceSink g_gemv_trace;
 
-template <int FMT, int R, int WAVES, int D, int XU, int NP>
+// DYN: the workgroup's row groups form one pool that its waves take from through an LDS
+// counter, one group at a time, instead of a fixed share per wave. The waves of a SIMD do
+// not progress at one rate (the oldest is served first: with 14 items each, the four waves
+// of a SIMD ended 9.4, 10.2, 11.7 and 12.7 us into a launch), so fixed shares end with the
+// slowest wave; from the pool, the faster waves take more groups. Every group is still
+// computed by one wave, its chunk steps in order, so results do not change. R = 1 only.
+template <int FMT, int R, int WAVES, int D, int XU, int NP, bool DYN = false>
 __global__ void __launch_bounds__(WAVES * 64)
 gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float *add, float *y, int groups, int st0,
             int KW, TraceSink trace) {
+    static_assert(!DYN || (R == 1 && (NP == 128 || NP == 480)), "pooled groups: one row per group, x barrier");
     extern __shared__ f32x4 lds[];
+    __shared__ int pool_next;  // DYN: the next pool index to hand out
     const uint64_t tt0 = trace.p ? wall_clock64() : 0;
     const int K = (int)m.cols, N = (int)m.rows;
     // blockIdx.y selects a batch row (each batch row streams W again; batched decode uses
@@ -440,6 +448,11 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
     // -> 5.25 us, q|k|v 6.59 -> 6.42 us; down (K = 14336, one workgroup per CU) 11.62 -> 11.53
     // us once the set loads' waits were right (before that, 1-2 % slower with it).
     if constexpr (NP == 128 || NP == 480) {
+        if constexpr (DYN) {
+            // every wave starts with pool index = its wave index; the rest is handed out
+            if (threadIdx.x == 0) pool_next = WAVES;
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the store is done before the barrier
+        }
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
@@ -449,9 +462,46 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
     // one set's loads after the other, as in the loop: with the sets' loads interleaved here
     // (q of both, then scales of both), the wait counts the compiler derives for the loop
     // from both paths into it waited, for a set's scales, for the next set's quants too
+    // DYN: the load position (group lg or -1 when the wave's work is over, chunk step lst);
+    // pool index k is group base + k % WAVES + (k / WAVES) nw, an increasing sequence, so the
+    // groups below `groups` are a prefix of k and a wave stops at its first index past it.
+    // A wave takes its next index when it starts loading a group (lane 0's LDS atomic) and
+    // reads the result only when that group's loads are all issued, so the atomic's latency
+    // hides behind a group's worth of items.
+    const int base = (int)blockIdx.x * WAVES;
+    int lg = gw < groups ? gw : -1, lst = 0, ktaken = 0;
+    int sg[D], sst[D];  // ring slot d: group (-1: absent) and chunk step of its item
+    auto load_next = [&](int d) __attribute__((always_inline)) {
+        // a wave-uniform branch, then the lane test on its own: folded into one test, the
+        // compiler computed (lst | lane) in the register of the row's pending y store and
+        // waited for that store before every group
+        if (lst == 0 && lg >= 0) {
+            asm volatile("");
+            if (lane == 0) ktaken = atomicAdd(&pool_next, 1);
+        }
+        sg[d] = lg;
+        sst[d] = lst;
+        const uint32_t row = (uint32_t)(lg >= 0 ? lg : 0);
+        Offs so;
+        so.qs = row * rowb.qs + (uint32_t)(lst + st0) * stepb.qs;
+        so.qh = row * rowb.qh + (uint32_t)(lst + st0) * stepb.qh;
+        so.sc = row * rowb.sc + (uint32_t)(lst + st0) * stepb.sc;
+        so.d = row * rowb.d + (uint32_t)(lst + st0) * stepb.d;
+        if (lg < 0) so = Offs{kOob, kOob, kOob, kOob};
+        set[d][0].load(rs, ln, so);
+        if (++lst == cpl) {
+            lst = 0;
+            if (lg >= 0) {
+                const int k = __builtin_amdgcn_readfirstlane(ktaken);
+                const int gn = base + k % WAVES + (k / WAVES) * nw;
+                lg = gn < groups ? gn : -1;
+            }
+        }
+    };
 #pragma unroll
     for (int d = 0; d < D; d++) {
-        load_item(d, set[d]);
+        if constexpr (DYN) load_next(d);
+        else load_item(d, set[d]);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -465,44 +515,81 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.f;
-    int step = 0, g = gw;
-    auto process = [&](const Chunk<FMT>(&ch)[R]) {
-        const int c = lane + 64 * step;
-        if (c < nchunks) {
-            XChunk xc;
-            const f32x4 *xp = xs + c;
+    int done = items;  // items this wave computed (trace)
+    if constexpr (!DYN) {
+        int step = 0, g = gw;
+        auto process = [&](const Chunk<FMT>(&ch)[R]) {
+            const int c = lane + 64 * step;
+            if (c < nchunks) {
+                XChunk xc;
+                const f32x4 *xp = xs + c;
 #pragma unroll
-            for (int j = 0; j < 8; j++) xc.v[j] = xp[j * NP];
-            const float2 sv = s16v[c];
+                for (int j = 0; j < 8; j++) xc.v[j] = xp[j * NP];
+                const float2 sv = s16v[c];
 #pragma unroll
-            for (int r = 0; r < R; r++) acc[r] = ch[r].apply(xc, f32x2{sv.x, sv.y}, acc[r], lane & 7);
-        }
-        if (++step == cpl) {
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float v = wave_sum(acc[r]);
-                const int row = __builtin_amdgcn_readfirstlane(g * R + r);
-                if (row < N) {
-                    // wave-uniform addresses: scalar loads. prev may be y itself: this wave
-                    // reads the element before its own lane 0 rewrites it.
-                    if (prev) v += prev[row];
-                    if (add) v += add[row];
-                    if (lane == 0) y[row] = v;
-                }
-                acc[r] = 0.f;
+                for (int r = 0; r < R; r++) acc[r] = ch[r].apply(xc, f32x2{sv.x, sv.y}, acc[r], lane & 7);
             }
-            step = 0;
-            g += nw;
-        }
-    };
-    // A set is only ever written by its own loads, so no in-flight load destination is
-    // copied, and consuming set d waits only for its own loads: the D - 1 other sets stay in
-    // flight.
-    for (int i = 0; i < items; i += D) {
+            if (++step == cpl) {
 #pragma unroll
-        for (int d = 0; d < D; d++) {
-            if (i + d < items) process(set[d]);
-            load_item(i + d + D, set[d]);
+                for (int r = 0; r < R; r++) {
+                    float v = wave_sum(acc[r]);
+                    const int row = __builtin_amdgcn_readfirstlane(g * R + r);
+                    if (row < N) {
+                        // wave-uniform addresses: scalar loads. prev may be y itself: this wave
+                        // reads the element before its own lane 0 rewrites it.
+                        if (prev) v += prev[row];
+                        if (add) v += add[row];
+                        if (lane == 0) y[row] = v;
+                    }
+                    acc[r] = 0.f;
+                }
+                step = 0;
+                g += nw;
+            }
+        };
+        // A set is only ever written by its own loads, so no in-flight load destination is
+        // copied, and consuming set d waits only for its own loads: the D - 1 other sets stay in
+        // flight.
+        for (int i = 0; i < items; i += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                if (i + d < items) process(set[d]);
+                load_item(i + d + D, set[d]);
+            }
+        }
+    } else {
+        auto process_slot = [&](int d) __attribute__((always_inline)) {
+            const int c = lane + 64 * sst[d];
+            if (c < nchunks) {
+                XChunk xc;
+                const f32x4 *xp = xs + c;
+#pragma unroll
+                for (int j = 0; j < 8; j++) xc.v[j] = xp[j * NP];
+                const float2 sv = s16v[c];
+                acc[0] = set[d][0].apply(xc, f32x2{sv.x, sv.y}, acc[0], lane & 7);
+            }
+            if (sst[d] == cpl - 1) {
+                float v = wave_sum(acc[0]);
+                const int row = sg[d];
+                if (prev) v += prev[row];
+                if (add) v += add[row];
+                if (lane == 0) y[row] = v;
+                acc[0] = 0.f;
+            }
+        };
+        // items in load order, item i in slot i % D, in the shape of the fixed-share loop; the
+        // first absent item ends the wave's work (every later one is absent too), so a round
+        // that starts with an absent slot 0 is past the end
+        done = 0;
+        while (sg[0] >= 0) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                if (sg[d] >= 0) {
+                    process_slot(d);
+                    done++;
+                }
+                load_next(d);
+            }
         }
     }
     if (trace.p && blockIdx.y == 0 && gw < trace.waves && lane == 0) {
@@ -510,16 +597,15 @@ gemv_kernel(QMat m, const float *__restrict__ x, const float *prev, const float 
         t[0] = tt0;
         t[1] = tt1;
         t[2] = wall_clock64();
-        t[3] = (uint64_t)(uint32_t)items | ((uint64_t)__smid() << 32);
+        t[3] = (uint64_t)(uint32_t)done | ((uint64_t)__smid() << 32);
     }
 }
 
-template <int FMT, int R, int WAVES, int D, int XU, int NP>
+template <int FMT, int R, int WAVES, int D, int XU, int NP, bool DYN = false>
 hipError_t launch_k(const QMat &m, const float *x, const float *prev, const float *add, float *y, int batch, int grid,
                     int groups, int st0, int kw, hipStream_t s) {
-    gemv_kernel<FMT, R, WAVES, D, XU, NP><<<dim3(grid, batch), WAVES * 64, XImage<NP>::kBytes, s>>>(m, x, prev, add, y,
-                                                                                                  groups, st0, kw,
-                                                                                                  g_gemv_trace);
+    gemv_kernel<FMT, R, WAVES, D, XU, NP, DYN><<<dim3(grid, batch), WAVES * 64, XImage<NP>::kBytes, s>>>(
+        m, x, prev, add, y, groups, st0, kw, g_gemv_trace);
     return hipGetLastError();
 }
 
@@ -529,7 +615,7 @@ constexpr int64_t kMaxWindow = 32768;
 
 // One launch over the column window [c0, c0 + kw) (c0 a multiple of 2048). The kernel is
 // instantiated for four x-image sizes: kw <= 4096, 8192, 15360 and 32768.
-template <int FMT, int R, int WAVES, int D>
+template <int FMT, int R, int WAVES, int D, bool DYN = false>
 hipError_t launch(const QMat &m, const float *x, const float *prev, const float *add, float *y, int batch, int wg_cap,
                   int64_t c0, int64_t kw, hipStream_t s) {
     const int groups = (int)((m.rows + R - 1) / R);
@@ -538,7 +624,9 @@ hipError_t launch(const QMat &m, const float *x, const float *prev, const float 
     constexpr int T = WAVES * 64;
     const int st0 = (int)(c0 / 2048), k = (int)kw;
     if (c0 % 2048 != 0 || kw % 32 != 0 || kw <= 0) return hipErrorInvalidValue;
-    if (kw <= 4096) return launch_k<FMT, R, WAVES, D, (1024 + T - 1) / T, 128>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
+    if (kw <= 4096)
+        return launch_k<FMT, R, WAVES, D, (1024 + T - 1) / T, 128, DYN>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
+    if constexpr (DYN) return hipErrorInvalidValue;  // pooled groups: windows of up to 4096 columns
     if (kw <= 8192) return launch_k<FMT, R, WAVES, D, (2048 + T - 1) / T, 256>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
     if (kw <= 15360) return launch_k<FMT, R, WAVES, D, (3840 + T - 1) / T, 480>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
     if (kw <= kMaxWindow) return launch_k<FMT, R, WAVES, D, (8192 + T - 1) / T, 1024>(m, x, prev, add, y, batch, grid, groups, st0, k, s);
