@@ -28,7 +28,10 @@ namespace {
 // workgroups per CU (the workgroups after the first on a CU stage x behind the weight
 // stream of those before them: against 4 per CU, the decode step 1.256-1.259 -> 1.249-1.251
 // ms by median over six A/B rounds on one box, Q4_K 14336 x 4096 9.2 -> 9.0 us; 1 or 3 per
-// CU and one 16-wave workgroup per CU were slower), or for matrices of at least 16384 rows one
+// CU and one 16-wave workgroup per CU were slower), its waves taking row groups from the
+// workgroup's pool (gemv_kernel DYN; against fixed shares, Q4_0 11008 x 4096 8.0 -> 7.6 us,
+// Q8_0 4096 x 4096 6.4 -> 6.2 us, Q4_K 14336 x 4096 9.0 -> 8.75 us, decode step 1.21 -> 1.19
+// ms; pooled 16-wave workgroups, one per CU, were slower), or for matrices of at least 16384 rows one
 // workgroup of 16 waves per CU (every CU stages x once, at the start: with two workgroups
 // per CU the second one's x loads queued behind the first one's weight stream; the
 // Llama-3-8B decode step 1.226-1.232 -> 1.213-1.219 ms in an A/B on one box, the fused
@@ -45,7 +48,7 @@ hipError_t launch_window(const QMat &m, const float *x, const float *prev, const
                          int cus, int64_t c0, int64_t kw, hipStream_t s) {
     if (kw <= 4096)
         return m.rows >= 16384 ? gemv::launch<FMT, 1, 16, 2, true>(m, x, prev, add, y, batch, cus, c0, kw, s)
-                               : gemv::launch<FMT, 1, 8, 2>(m, x, prev, add, y, batch, 2 * cus, c0, kw, s);
+                               : gemv::launch<FMT, 1, 8, 2, true>(m, x, prev, add, y, batch, 2 * cus, c0, kw, s);
     if (kw <= 8192) return gemv::launch<FMT, 1, 8, 2>(m, x, prev, add, y, batch, 2 * cus, c0, kw, s);
     return gemv::launch<FMT, 1, 16, 2>(m, x, prev, add, y, batch, cus, c0, kw, s);
 }
