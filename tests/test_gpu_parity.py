@@ -302,6 +302,48 @@ def test_gemv_batched_wide_k(backend, uploaded, qt, rows, cols, B):
         backend.release(h)
 
 
+# 9-16 batch rows over K = 4096 run two 2048-column windows, each in its own workgroups, and
+# sum_windows_kernel adds their sums in window order: y equals, bit for bit, fl(y_left +
+# y_right) of the two column halves uploaded as matrices of their own (one window each, the
+# same waves' slices of x), and the add joins on its own. The row counts give 19 to 2500
+# tiles: one to ten per workgroup, partial rounds and the ring's second slot empty.
+HALVES_CASES = [
+    (QuantType.Q8_0, 300), (QuantType.Q4_K, 4096), (QuantType.Q4_K, 6144), (QuantType.Q4_0, 11008),
+    (QuantType.Q6_K, 11008), (QuantType.Q4_K, 28672 + 48), (QuantType.Q8_0, 28672 + 48), (QuantType.Q4_K, 40000),
+]
+
+
+@pytest.mark.parametrize("qt,rows", HALVES_CASES, ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [9, 16])
+def test_gemv_batched_two_windows_equal_sum_of_halves(backend, qt, rows, B):
+    cols, half = 4096, 2048
+    note("batched halves", qt.name, rows, cols, "B", B)
+    blob = S.quant_blocks(qt, 0x4A1F + rows, rows, cols)
+    per_row = cols // qt.block_elements * qt.block_bytes
+    grid = np.frombuffer(blob, dtype=np.uint8).reshape(rows, per_row)
+    left = np.ascontiguousarray(grid[:, : per_row // 2]).tobytes()
+    right = np.ascontiguousarray(grid[:, per_row // 2:]).tobytes()
+    w = backend.upload_quantized(blob, qt, (rows, cols))
+    wl = backend.upload_quantized(left, qt, (rows, half))
+    wr = backend.upload_quantized(right, qt, (rows, half))
+    xs = S.activations_f32(rows + 3 * B, B * cols).reshape(B, cols)
+    add = S.activations_f32(rows + 17, B * rows).reshape(B, rows)
+    xb = backend.upload(xs, shape=(B, cols))
+    xlb = backend.upload(np.ascontiguousarray(xs[:, :half]), shape=(B, half))
+    xrb = backend.upload(np.ascontiguousarray(xs[:, half:]), shape=(B, half))
+    ab = backend.upload(add, shape=(B, rows))
+    y, ya = backend.quant_matvec(w, xb), backend.quant_matvec_add(w, xb, ab)
+    yl, yr = backend.quant_matvec(wl, xlb), backend.quant_matvec(wr, xrb)
+    got = backend.download(y).reshape(B, rows)
+    halves = backend.download(yl).reshape(B, rows) + backend.download(yr).reshape(B, rows)
+    assert np.array_equal(bits(got), bits(halves))
+    assert np.array_equal(bits(backend.download(ya).reshape(B, rows)), bits(got + add))
+    y64 = oracle.matvec_f64(qt.id, blob, rows, cols, xs[B - 1])
+    assert rel_err(got[B - 1], y64) <= 4e-5
+    for h in (w, wl, wr, xb, xlb, xrb, ab, y, ya, yl, yr):
+        backend.release(h)
+
+
 @pytest.mark.parametrize("cols", [4096, 11008])
 @pytest.mark.parametrize("B", [8, 16])
 @pytest.mark.parametrize("shift", [0, 1])
