@@ -558,6 +558,49 @@ def test_gemv_any_k(backend, uploaded, qt, rows, cols, B):
         backend.release(h)
 
 
+# Batch rows of 1-2 over 8193..15360 columns (one 16-wave workgroup per CU, a 480-chunk x
+# image): rows below one workgroup's 16 and not a multiple of it, a partial last step
+# (K = 9024: 26 chunks in the last step of 64) and 40000 rows (ten per wave). Checked
+# against the fp64 oracle, bit-identical on repeated calls and under an exact scaling of x,
+# the add rounded on its own, and y updated in place on the add buffer.
+WIDE_WINDOW_CASES = [
+    (QuantType.Q6_K, 1, 14336), (QuantType.Q6_K, 13, 14336), (QuantType.Q6_K, 4096 + 5, 14336),
+    (QuantType.Q4_K, 300, 9216), (QuantType.Q4_0, 700, 9024), (QuantType.Q8_0, 200, 15360),
+    (QuantType.Q2_0, 100, 11008), (QuantType.Q6_K, 40000, 14336),
+]
+
+
+@pytest.mark.parametrize("qt,rows,cols", WIDE_WINDOW_CASES, ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [1, 2])
+def test_gemv_wide_window_b1(backend, qt, rows, cols, B):
+    note("wide window", qt.name, rows, cols, "B", B)
+    blob = S.quant_blocks(qt, 0x57E9 + rows + cols, rows, cols)
+    w = backend.upload_quantized(blob, qt, (rows, cols))
+    xs = S.activations_f32(rows + 23 * B, B * cols).reshape(B, cols)
+    add = S.activations_f32(rows + 29, B * rows).reshape(B, rows)
+    shape_x, shape_y = ((B, cols), (B, rows)) if B > 1 else (None, None)
+    xb = backend.upload(xs if B > 1 else xs[0], shape=shape_x)
+    ab = backend.upload(add if B > 1 else add[0], shape=shape_y)
+    y, y2 = backend.quant_matvec(w, xb), backend.quant_matvec(w, xb)
+    ya = backend.quant_matvec_add(w, xb, ab)
+    got = backend.download(y).reshape(B, rows)
+    ref = oracle.matmul_f64(qt.id, blob, rows, cols, xs)
+    for b in range(B):
+        assert rel_err(got[b], ref[b]) <= 1e-5, f"row {b}"
+    assert np.array_equal(bits(backend.download(y2).reshape(B, rows)), bits(got))
+    assert np.array_equal(bits(backend.download(ya).reshape(B, rows)), bits(got + add))
+    xd = backend.upload(2.0 * xs if B > 1 else 2.0 * xs[0], shape=shape_x)
+    yd = backend.quant_matvec(w, xd)
+    assert np.array_equal(bits(backend.download(yd).reshape(B, rows)), bits(2.0 * got))
+    res = backend.upload(add.reshape(-1))
+    rp = backend.buffer_desc(res).device_ptr
+    backend.quant_matvec_into(w, backend.buffer_desc(xb).device_ptr, rp, rp, B)
+    backend.sync()
+    assert np.array_equal(bits(backend.download(res).reshape(B, rows)), bits(got + add))
+    for h in (w, xb, ab, y, y2, ya, xd, yd, res):
+        backend.release(h)
+
+
 def test_in_place_add_wider_than_one_window_is_rejected(backend, uploaded):
     """An add that overlaps y is read after the first window rewrote y, so above 32768 columns
     the stream-ordered entry point refuses it (the SPI's quantMatvecAdd always returns a new
