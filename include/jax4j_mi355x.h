@@ -53,6 +53,8 @@ enum j4q_kind { J4Q_KIND_QUANT = 1, J4Q_KIND_F32 = 2, J4Q_KIND_BF16 = 3, J4Q_KIN
 
 /* Prefill GEMM variants (engine-local; the SPI has no matmul over quantized weights). */
 enum j4q_gemm_variant { J4Q_GEMM_INT8 = 0, J4Q_GEMM_BF16 = 1 };
+/* Arithmetic of batched GEMV (j4q_set_gemv_policy). */
+enum j4q_gemv_policy { J4Q_GEMV_MATRIX_CORES = 0, J4Q_GEMV_FP32 = 1 };
 
 typedef uint64_t j4q_buffer; /* 0 is never a valid handle */
 
@@ -156,6 +158,18 @@ int j4q_quant_matvec_add(j4q_buffer weights, j4q_buffer x, j4q_buffer add, j4q_b
 int j4q_quant_gather_row(j4q_buffer weights, int64_t row, j4q_buffer *y);
 /* Whole-matrix dequantization to F32 [rows, cols], bit-exact (engine-local export). */
 int j4q_quant_dequantize(j4q_buffer weights, j4q_buffer *y);
+/* Arithmetic of batched GEMV, x [B, cols] with B >= 3 (engine-local; the SPI's quantMatvec is
+ * one row, CpuBackend.java:712, and the engine's batch is row b = quantMatvec of x[b]):
+ *  J4Q_GEMV_MATRIX_CORES (default): launches of up to 16 batch rows on the matrix cores (Q8_0,
+ *    Q4_0, Q4_K, Q6_K), W streamed once per launch; x enters the products as hi + lo fp16
+ *    (22 significant bits under a power-of-two scale), the products are exact, and each row
+ *    stays within 1e-4 of the fp64 product (within 4e-5 up to K = 40960 in the tests);
+ *  J4Q_GEMV_FP32: every batch row on the batch-1 kernel (fp32 x, fp32 accumulation, no
+ *    matrix cores; W streamed once per row), so row b equals quantMatvec of x[b] bit for bit.
+ * Process-wide, for every call issued afterwards; a decode plan keeps the launches it
+ * captured at creation. *previous (may be NULL) receives the policy it replaces. An unknown
+ * policy: J4Q_EINVAL, nothing changed. */
+int j4q_set_gemv_policy(int policy, int *previous);
 
 /* ---- prefill GEMM (engine-local; no SPI counterpart, see CpuBackend.java:712) ---------- */
 

@@ -1,6 +1,7 @@
 package com.nablatensor.jax4j.backend.mi355x;
 
 import static java.lang.foreign.ValueLayout.JAVA_FLOAT;
+import static java.lang.foreign.ValueLayout.JAVA_INT;
 import static java.lang.foreign.ValueLayout.JAVA_LONG;
 import static java.lang.foreign.ValueLayout.JAVA_SHORT;
 
@@ -174,6 +175,19 @@ public final class Mi355xBackend implements ComputeBackend, QuantizedOps {
     requireBatch(w, x, "quantMatvecAddBatched");
     long h = newHandle("quantMatvecAddBatched", Mi355xNative.MATVEC_ADD, w.handle, buf(x).handle, buf(add).handle);
     return new Mi355xBuffer(h, Shape.of(x.shape().dim(0), w.shape().dim(0)), DType.F32, w.device(), null);
+  }
+
+  /** Arithmetic of the batched calls above, process-wide (j4q_set_gemv_policy): false (the
+   *  default) runs up to 16 batch rows per pass on the matrix cores, x as hi + lo fp16 under a
+   *  power-of-two scale; true runs every row on the batch-1 kernel (fp32 x, no matrix cores),
+   *  each row equal bit for bit to quantMatvec of that row. Returns the previous setting. */
+  public boolean batchedGemvFp32(boolean fp32) {
+    try (Arena a = Arena.ofConfined()) {
+      MemorySegment prev = a.allocate(JAVA_INT);
+      Mi355xNative.call("setGemvPolicy", Mi355xNative.SET_GEMV_POLICY,
+          fp32 ? Mi355xNative.GEMV_FP32 : Mi355xNative.GEMV_MATRIX_CORES, prev);
+      return prev.get(JAVA_INT, 0) == Mi355xNative.GEMV_FP32;
+    }
   }
 
   private static void requireBatch(Mi355xBuffer w, DeviceBuffer x, String op) {

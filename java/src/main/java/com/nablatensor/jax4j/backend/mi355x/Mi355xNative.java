@@ -25,6 +25,8 @@ final class Mi355xNative {
   static final int OK = 0, EINVAL = 1, EUNSUPPORTED = 2, ENODEV = 3, EHIP = 4, ENOMEM = 5, EHANDLE = 6;
   /** Prefill GEMM variants (enum j4q_gemm_variant). */
   static final int GEMM_INT8 = 0, GEMM_BF16 = 1;
+  /** Batched GEMV arithmetic (enum j4q_gemv_policy). */
+  static final int GEMV_MATRIX_CORES = 0, GEMV_FP32 = 1;
   /** j4q_buffer_desc: 48 bytes; dims at 16 and 24, device_ptr at 40. */
   static final long BUFFER_DESC_BYTES = 48, DESC_DIM0 = 16, DESC_DIM1 = 24, DESC_DEVICE_PTR = 40;
 
@@ -66,6 +68,8 @@ final class Mi355xNative {
       FunctionDescriptor.of(JAVA_INT, JAVA_LONG, JAVA_LONG, JAVA_LONG, ADDRESS));
   static final MethodHandle GATHER_ROW = fn("j4q_quant_gather_row",
       FunctionDescriptor.of(JAVA_INT, JAVA_LONG, JAVA_LONG, ADDRESS));
+  static final MethodHandle SET_GEMV_POLICY = fn("j4q_set_gemv_policy",
+      FunctionDescriptor.of(JAVA_INT, JAVA_INT, ADDRESS));
   static final MethodHandle MATMUL = fn("j4q_quant_matmul",
       FunctionDescriptor.of(JAVA_INT, JAVA_LONG, JAVA_LONG, JAVA_INT, ADDRESS));
   static final MethodHandle CONCAT_ROWS = fn("j4q_concat_rows",

@@ -27,6 +27,9 @@ KIND_I8 = 4
 
 GEMM_INT8 = 0
 GEMM_BF16 = 1
+# j4q_gemv_policy
+GEMV_MATRIX_CORES = 0
+GEMV_FP32 = 1
 
 
 class DeviceProps(C.Structure):
@@ -131,6 +134,7 @@ SIGNATURES = {
     "j4q_quant_matvec_add": [_buf, _buf, _buf, _pbuf],
     "j4q_quant_gather_row": [_buf, _i64, _pbuf],
     "j4q_quant_dequantize": [_buf, _pbuf],
+    "j4q_set_gemv_policy": [C.c_int, C.POINTER(C.c_int)],
     "j4q_quantize_act": [_buf, _pbuf, _pbuf],
     "j4q_quant_matmul": [_buf, _buf, C.c_int, _pbuf],
     "j4q_quant_matvec_into": [_buf, _vp, _vp, _vp, _i64, _vp],

@@ -213,6 +213,18 @@ class Mi355xBackend:
             DeviceBuffer(s.value, (m, k // 32), DType.F32, x.device),
         )
 
+    def set_gemv_policy(self, policy: str) -> str:
+        """Arithmetic of batched GEMV (engine-local): "matrix_cores" (default; launches of up
+        to 16 batch rows, x as hi + lo fp16) or "fp32" (every row on the batch-1 kernel, equal
+        bit for bit to quantMatvec of that row). Process-wide; returns the policy replaced."""
+        names = {"matrix_cores": N.GEMV_MATRIX_CORES, "fp32": N.GEMV_FP32}
+        if policy not in names:
+            raise IllegalArgumentException(f"unknown GEMV policy {policy!r} (matrix_cores or fp32)")
+        prev = C.c_int()
+        # a process-wide setting of the library: no device needed
+        check(N.load().j4q_set_gemv_policy(names[policy], C.byref(prev)), "setGemvPolicy")
+        return {v: k for k, v in names.items()}[prev.value]
+
     def dequantize(self, weights: DeviceBuffer) -> DeviceBuffer:
         out = C.c_uint64()
         check(self._lib().j4q_quant_dequantize(weights.handle, C.byref(out)), "dequantize")

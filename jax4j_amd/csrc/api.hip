@@ -723,6 +723,15 @@ int j4q_quant_matvec_add(j4q_buffer w, j4q_buffer x, j4q_buffer add, j4q_buffer 
     return matvec_common(w, x, add, y, "quantMatvecAdd");
 }
 
+int j4q_set_gemv_policy(int policy, int *previous) {
+    if (policy != J4Q_GEMV_MATRIX_CORES && policy != J4Q_GEMV_FP32)
+        return fail(J4Q_EINVAL, "set_gemv_policy: unknown policy %d (J4Q_GEMV_MATRIX_CORES or J4Q_GEMV_FP32)", policy);
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (previous) *previous = j4q::gemv_policy();
+    j4q::gemv_set_policy(policy);
+    return J4Q_OK;
+}
+
 int j4q_quant_gather_row(j4q_buffer wh, int64_t row, j4q_buffer *out) {
     if (!out) return fail(J4Q_EINVAL, "quantGatherRow: out is NULL");
     std::lock_guard<std::mutex> lk(g_mu);

@@ -1,7 +1,10 @@
 // Decode GEMV dispatch: picks the row-group size R, waves per workgroup and grid size of
 // the persistent GEMV kernel (gemv_impl.h) for each format and shape.
+#include <atomic>
+
 #include "gemv_impl.h"
 #include "gemv_mfma.h"
+#include "jax4j_mi355x.h"
 
 namespace j4q {
 namespace gemv {
@@ -287,12 +290,23 @@ void gemv_set_cus(int cus) {
     measure_resident_fmt<Q6_K>();
 }
 
+namespace {
+std::atomic<int> g_gemv_policy{J4Q_GEMV_MATRIX_CORES};
+// whether a batch of `batch` rows runs on the matrix cores
+bool on_matrix_cores(int id, const QMat &m, int64_t batch) {
+    return batch >= 3 && mfma_format(id, m) && g_gemv_policy.load(std::memory_order_relaxed) == J4Q_GEMV_MATRIX_CORES;
+}
+}  // namespace
+
+void gemv_set_policy(int policy) { g_gemv_policy.store(policy, std::memory_order_relaxed); }
+int gemv_policy() { return g_gemv_policy.load(std::memory_order_relaxed); }
+
 bool gemv_in_place_ok(int id, const QMat &m, int64_t batch) {
-    return m.cols <= gemv::kMaxWindow || (batch >= 3 && mfma_format(id, m));
+    return m.cols <= gemv::kMaxWindow || on_matrix_cores(id, m, batch);
 }
 
 uint64_t gemv_workspace_bytes(int id, const QMat &m, int64_t batch) {
-    if (batch < 3 || m.rows <= 0 || !mfma_format(id, m)) return 0;
+    if (m.rows <= 0 || !on_matrix_cores(id, m, batch)) return 0;
     // launches of 16 rows and, for a remainder of 3..15 rows, one smaller launch
     uint64_t need = mfma_ws_any(id, m, (int)(batch < 16 ? batch : 16));
     const int64_t rem = batch % 16;
@@ -313,7 +327,7 @@ hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, 
     if (m.rows <= 0 || batch <= 0) return hipSuccess;
     if (batch > 65535 || m.rows > (1 << 30) || m.cols > 0x7fffffff) return hipErrorInvalidValue;
     const bool alias = add && add < y + batch * m.rows && y < add + batch * m.rows;
-    const bool mfma = batch >= 3 && mfma_format(id, m);
+    const bool mfma = on_matrix_cores(id, m, batch);
     // with the workspace, several windows meet in sum_windows_kernel, which reads each add
     // element before it writes y there; without it they are chained launches that would
     // read an add overlapping y after rewriting y, so such a call keeps one window

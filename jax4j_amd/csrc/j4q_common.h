@@ -136,6 +136,10 @@ uint64_t gemv_workspace_bytes(int id, const QMat &m, int64_t batch);
 // Whether an add that overlaps y is served for this matrix and batch (given the workspace
 // gemv_workspace_bytes asks for): one column window, or the matrix-core path.
 bool gemv_in_place_ok(int id, const QMat &m, int64_t batch);
+// Batched GEMV arithmetic (J4Q_GEMV_MATRIX_CORES or J4Q_GEMV_FP32), process-wide; launches
+// read it when they are issued.
+void gemv_set_policy(int policy);
+int gemv_policy();
 hipError_t launch_gemv(int id, const QMat &m, const float *x, const float *add, float *y, int64_t batch,
                        hipStream_t s, const Workspace &ws = Workspace());
 hipError_t launch_quantize_act(const uint16_t *x, int64_t m, int64_t k, int8_t *q, float *scales,

@@ -106,6 +106,23 @@ def test_raw_entry_points_check_alignment_and_batch():
     assert rc == N.J4Q_EINVAL
 
 
+def test_gemv_policy_round_trip_and_unknown_policy():
+    lib = N.load()
+    prev = C.c_int(-1)
+    assert lib.j4q_set_gemv_policy(7, C.byref(prev)) == N.J4Q_EINVAL and "policy" in N.last_error()
+    assert prev.value == -1  # nothing changed, nothing written
+    assert lib.j4q_set_gemv_policy(N.GEMV_FP32, C.byref(prev)) == N.J4Q_OK
+    assert prev.value == N.GEMV_MATRIX_CORES
+    assert lib.j4q_set_gemv_policy(N.GEMV_MATRIX_CORES, None) == N.J4Q_OK
+    assert lib.j4q_set_gemv_policy(N.GEMV_MATRIX_CORES, C.byref(prev)) == N.J4Q_OK
+    assert prev.value == N.GEMV_MATRIX_CORES
+    be = B.Mi355xBackend.__new__(B.Mi355xBackend)  # the setter needs no device
+    with pytest.raises(IllegalArgumentException):
+        be.set_gemv_policy("bf16")
+    assert be.set_gemv_policy("fp32") == "matrix_cores"
+    assert be.set_gemv_policy("matrix_cores") == "fp32"
+
+
 def test_error_mapping_follows_reference_exception_types():
     with pytest.raises(IllegalArgumentException):
         B.check(N.J4Q_EINVAL, "x")

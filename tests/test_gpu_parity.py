@@ -601,6 +601,47 @@ def test_gemv_wide_window_b1(backend, qt, rows, cols, B):
         backend.release(h)
 
 
+# J4Q_GEMV_FP32: batched GEMV runs every row on the batch-1 kernel (fp32 x, fp32 accumulation,
+# no matrix cores), so each row equals quantMatvec of that row alone bit for bit, with the add
+# on its own and in place; B = 3 and 17 would otherwise take the matrix cores (17: a 16-row
+# launch and a remainder). K = 40960 runs chained column windows.
+@pytest.mark.parametrize("qt,rows,cols", [(QuantType.Q4_K, 300, 4096), (QuantType.Q6_K, 200, 14336),
+                                          (QuantType.Q4_0, 257, 4096), (QuantType.Q8_0, 64, 40960)],
+                         ids=lambda v: getattr(v, "name", str(v)))
+@pytest.mark.parametrize("B", [3, 17])
+def test_gemv_fp32_policy_rows_equal_single_calls(backend, qt, rows, cols, B):
+    note("fp32 policy", qt.name, rows, cols, "B", B)
+    prev = backend.set_gemv_policy("fp32")
+    handles = []
+    try:
+        blob = S.quant_blocks(qt, 0xF32 + rows + cols, rows, cols)
+        w = backend.upload_quantized(blob, qt, (rows, cols))
+        xs = S.activations_f32(rows + 31 * B, B * cols).reshape(B, cols)
+        add = S.activations_f32(rows + 37, B * rows).reshape(B, rows)
+        xb, ab = backend.upload(xs, shape=(B, cols)), backend.upload(add, shape=(B, rows))
+        y, ya = backend.quant_matvec(w, xb), backend.quant_matvec_add(w, xb, ab)
+        handles += [w, xb, ab, y, ya]
+        got = backend.download(y).reshape(B, rows)
+        for b in range(B):
+            xr = backend.upload(xs[b])
+            yr = backend.quant_matvec(w, xr)
+            handles += [xr, yr]
+            assert np.array_equal(bits(backend.download(yr)), bits(got[b])), f"row {b}"
+        assert np.array_equal(bits(backend.download(ya).reshape(B, rows)), bits(got + add))
+        assert rel_err(got[0], oracle.matvec_f64(qt.id, blob, rows, cols, xs[0])) <= 1e-5
+        if cols <= 32768:
+            res = backend.upload(add.reshape(-1))
+            handles.append(res)
+            rp = backend.buffer_desc(res).device_ptr
+            backend.quant_matvec_into(w, backend.buffer_desc(xb).device_ptr, rp, rp, B)
+            backend.sync()
+            assert np.array_equal(bits(backend.download(res).reshape(B, rows)), bits(got + add))
+    finally:
+        backend.set_gemv_policy(prev)
+        for h in handles:
+            backend.release(h)
+
+
 def test_in_place_add_wider_than_one_window_is_rejected(backend, uploaded):
     """An add that overlaps y is read after the first window rewrote y, so above 32768 columns
     the stream-ordered entry point refuses it (the SPI's quantMatvecAdd always returns a new
