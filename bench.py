@@ -366,8 +366,11 @@ def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n:
         if rc:
             check(rc, "gemm")
 
+    # us_per_call from a region with events at its ends only; median / min / p90 from a second
+    # region split into SAMPLES parts (each inner event adds a gap to the stream), as for the GEMVs
     _, _, _, host_us, _ = eng.time_region(enqueue, warmup)
-    ms, sms, cnt, _, host_bound = eng.time_region(enqueue, steps, host_us, SAMPLES)
+    ms, _, _, _, host_bound = eng.time_region(enqueue, steps, host_us)
+    _, sms, cnt, _, _ = eng.time_region(enqueue, steps, host_us, SAMPLES)
     per = ms / steps
     ops = 2.0 * m * n * k
     tops = ops / (per * 1e-3) / 1e12
