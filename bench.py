@@ -400,6 +400,42 @@ def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n:
     }
 
 
+def gemm_regions(eng: Engine, m: int, variant: str, steps_list=(20, 40, 75, 200), idle_us: int = 50_000):
+    """The Q8_0 GEMM of configs[3] at M = m in regions of back-to-back calls (steps_list), each
+    after `idle_us` of a one-workgroup spin (the matrix cores idle), with events at the quarters
+    of each region: how the time per call moves with the length of a sustained run."""
+    n = k = 4096
+    qt = QuantType.Q8_0
+    copies = max(1, math.ceil(ROTATE_BYTES / qt.byte_size_for(n * k)))
+    ws = [eng.weights(qt, n, k, 0x5EED8 + 31 * i)[0] for i in range(copies)]
+    x = eng.bf16(m * k, 0x5EED9)
+    xq, xs, y = eng.hip.malloc(m * k), eng.hip.malloc(4 * m * (k // 32)), eng.hip.malloc(4 * m * n)
+    handles = [w.handle for w in ws]
+    fn = eng.lib.j4q_quant_matmul_into
+    v = N.GEMM_INT8 if variant == "int8" else N.GEMM_BF16
+    s = C.c_void_p(eng.stream)
+    xp, xqp, xsp, yp = C.c_void_p(x), C.c_void_p(xq), C.c_void_p(xs), C.c_void_p(y)
+
+    def enqueue(i):
+        rc = fn(handles[i % copies], xp, m, v, xqp, xsp, yp, s)
+        if rc:
+            check(rc, "gemm")
+
+    _, _, _, host_us, _ = eng.time_region(enqueue, 10)
+    out = []
+    for calls in steps_list:
+        check(eng.lib.j4q_spin(idle_us, s), "spin")
+        ms, sms, cnt, _, _ = eng.time_region(enqueue, calls, host_us, 4)
+        quarters = [round(1e3 * t / c, 2) for t, c in zip(sms, cnt)]
+        out.append({"calls": calls, "us_per_call": round(1e3 * ms / calls, 2), "quarters_us": quarters})
+        log(f"gemm {variant} M={m}, region of {calls} calls: {1e3 * ms / calls:.2f} us per call; quarters {quarters}")
+    for w in ws:
+        eng.be.release(w)
+    for p in (x, xq, xs, y):
+        eng.hip.free(p)
+    return {"workload": f"q8_0_gemm_{variant}_m{m}", "idle_us_before_each": idle_us, "regions": out}
+
+
 def timeline_workload(eng: Engine, name: str, qt: QuantType, rows: int, cols: int, parts=None, launches: int = 40):
     """Per-wave timeline of one batch-1 GEMV launch (j4q_gemv_trace): `launches` back-to-back
     launches over rotating weight copies, the last one traced. Reports, in us from the first
@@ -702,6 +738,9 @@ def main():
     ap.add_argument("--torch-reader", default="", metavar="BYTES,...",
                     help="only run PyTorch's torch.sum over rotating tensors of these sizes, in this process "
                          "(--calibrate runs it as a child process)")
+    ap.add_argument("--gemm-regions", action="store_true",
+                    help="also time the bf16 and int8 Q8_0 GEMM at M = 2048 and 512 in regions of 20 to 200 calls "
+                         "after an idle spin (time per call against the length of a sustained run)")
     ap.add_argument("--timeline", action="store_true",
                     help="also record the per-wave timeline of one launch of the dominant GEMV and of the step's "
                          "smaller B = 1 GEMVs (j4q_gemv_trace)")
@@ -734,6 +773,9 @@ def main():
     model.release()
     dominant = gemv_workload(eng, DOMINANT, Q4K, 28672, 4096, 1, args.steps, args.warmup, parts=[14336, 14336])
     cal = calibrate(eng, args.steps, args.warmup) if args.calibrate else None
+    regions = None
+    if args.gemm_regions:
+        regions = [gemm_regions(eng, m, var) for m, var in ((2048, "bf16"), (2048, "int8"), (512, "bf16"))]
     timeline = None
     if args.timeline:
         khz = C.c_int()
@@ -805,6 +847,7 @@ def main():
         "cpu_rows": cpu_all,
         "calibration": cal,
         "timeline": timeline,
+        "gemm_regions": regions,
         "host": host_description(),
         "device": eng.info,
     }
