@@ -751,7 +751,7 @@ def main():
     if args.gpus != 1:
         print(
             f"bench.py: this engine is measured on one GPU; --gpus {args.gpus} is not supported "
-            "(the path would shard GEMV rows across GPUs, see DESIGN.md)",
+            "(across GPUs the path would shard the GEMV rows, gather y and replicate x)",
             file=sys.stderr,
         )
         sys.exit(2)
