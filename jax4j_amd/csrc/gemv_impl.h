@@ -2,8 +2,9 @@
 //
 // HBM-bound: every weight byte is read exactly once with a buffer load (128-bit for the
 // quant payload), and no MFMA is used. The kernel is persistent: a grid of a few hundred
-// workgroups stages x once into LDS, then each wave streams row groups g = wave, wave +
-// total_waves, ... of R consecutive rows. Lane l handles the 32-element chunks
+// workgroups stages x once into LDS, then each wave streams row groups of R consecutive rows,
+// either a fixed share g = wave, wave + total_waves, ... or (DYN) the next group of its
+// workgroup's share from a pool in LDS. Lane l handles the 32-element chunks
 // c = l, l + 64, ... of the group's rows, so one wave-wide load moves 64 x 16 contiguous bytes
 // of a row. Work items (group, chunk step) form one flat stream per wave; the loads of item
 // i + 1 are in flight while item i is computed, and the first item's loads are issued before
