@@ -243,6 +243,47 @@ def test_decode_plan_column_windows(backend, wide_model, B):
     check_plan(backend, wide_model, B, WIDE)
 
 
+def test_decode_plan_keeps_its_launches_across_gemv_policies(backend, model):
+    """A plan replays the launches it captured: one built on the matrix cores still equals the
+    eager calls on the matrix cores after j4q_set_gemv_policy switched to the fp32 kernel, and
+    one built under the fp32 policy equals the eager calls under it."""
+    B = 3
+    note("decode plan across GEMV policies", "B", B)
+    layers, _, head, _ = model
+    lib = N.load()
+    h0, xo, xd, bufs = make_io(backend, B)
+    io = {k: ptr(backend, bufs[k]) for k in ("h", "x_o", "x_down", "qkv", "gate_up", "logits")}
+
+    def replay(plan):
+        assert lib.j4q_copy(C.c_void_p(io["h"]), C.c_void_p(ptr(backend, bufs["h0"])), B * SMALL.D * 4, None) == 0
+        plan.run()
+        backend.sync()
+        return read(backend, bufs, B)
+
+    prev = backend.set_gemv_policy("matrix_cores")
+    plans = []
+    try:
+        plans.append(backend.decode_plan(layers, head, B, io))
+        ref_mc = eager(backend, layers, head, h0, xo, xd)
+        backend.set_gemv_policy("fp32")
+        plans.append(backend.decode_plan(layers, head, B, io))
+        ref_fp = eager(backend, layers, head, h0, xo, xd)
+        for plan, ref, tag in ((plans[0], ref_mc, "matrix cores"), (plans[1], ref_fp, "fp32")):
+            for name, g, e in zip(("h", "qkv", "gate_up", "logits"), replay(plan), ref):
+                assert np.array_equal(bits(g), bits(e)), f"{tag} plan: {name} differs from its eager calls"
+        # the fp32 policy's rows are the single-row calls
+        sh, sq, sg, sl = eager(backend, layers, head, h0[:1], xo[:1], xd[:1])
+        fh, fq, fg, fl = ref_fp
+        assert np.array_equal(bits(fh[0]), bits(sh[0])) and np.array_equal(bits(fl[0]), bits(sl[0]))
+        assert np.array_equal(bits(fq[:, 0]), bits(sq[:, 0])) and np.array_equal(bits(fg[:, 0]), bits(sg[:, 0]))
+    finally:
+        backend.set_gemv_policy(prev)
+        for plan in plans:
+            plan.destroy()
+        for b in bufs.values():
+            backend.release(b)
+
+
 def test_decode_plan_errors(backend, model):
     layers, _, head, _ = model
     B = 1
