@@ -54,6 +54,13 @@ LLAMA3_8B_HEAD = (Q6K, 128256, 4096)
 # GEMV, 28672 x 4096 Q4_K at batch 1. Its HBM bytes per launch were measured with rocprofv3
 # FETCH_SIZE / WRITE_SIZE counters scaled by a copy kernel of known size (see the .md beside it).
 DOMINANT = "q4_k_gemv_gate_up_fused_b1"
+# the decode step's four batch-1 GEMV shapes (name, type, rows, cols, concatenated parts)
+STEP_SHAPES_B1 = (
+    (DOMINANT, Q4K, 28672, 4096, [14336, 14336]),
+    ("q4_k_gemv_qkv_fused_b1", Q4K, 6144, 4096, [4096, 1024, 1024]),
+    ("q4_k_gemv_o_b1", Q4K, 4096, 4096, None),
+    ("q6_k_gemv_down_b1", Q6K, 4096, 14336, None),
+)
 # hipDeviceAttribute_t value of hipDeviceAttributeWallClockRate (kHz of the clock j4q_gemv_trace stamps)
 HIP_ATTR_WALL_CLOCK_RATE = 10017
 
@@ -187,14 +194,15 @@ class Engine:
 
 
 def gemv_workload(eng: Engine, name: str, qt: QuantType, rows: int, cols: int, batch: int, steps: int, warmup: int,
-                  parts=None):
+                  parts=None, rotate_bytes: int = ROTATE_BYTES):
     """GEMV launches over rotating weight copies. `parts` (row counts) builds each copy as a
     row concatenation (j4q_concat_rows), as the decode step fuses gate|up. us_per_launch comes
     from one region of `steps` back-to-back launches with events only at its ends (the
     rocprofv3 kernel average agrees with it); median / min / p90 come from a second region
-    split into SAMPLES parts, whose inner events each add a small gap to the stream."""
+    split into SAMPLES parts, whose inner events each add a small gap to the stream.
+    rotate_bytes = 1 keeps one copy, which then stays in the Infinity Cache between launches."""
     blob_bytes = qt.byte_size_for(rows * cols)
-    copies = max(1, math.ceil(ROTATE_BYTES / blob_bytes))
+    copies = max(1, math.ceil(rotate_bytes / blob_bytes))
     log(f"{name}: {qt.name} N={rows} K={cols} B={batch}, {copies} weight copies")
     ws = []
     for i in range(copies):
@@ -741,6 +749,10 @@ def main():
     ap.add_argument("--gemm-regions", action="store_true",
                     help="also time the bf16 and int8 Q8_0 GEMM at M = 2048 and 512 in regions of 20 to 200 calls "
                          "after an idle spin (time per call against the length of a sustained run)")
+    ap.add_argument("--resident", action="store_true",
+                    help="also time the decode step's four B = 1 GEMV shapes with one weight copy launched back to "
+                         "back (the weights stay in the 256 MB Infinity Cache) beside the same shapes over "
+                         "rotating copies: how much of each launch HBM accounts for")
     ap.add_argument("--timeline", action="store_true",
                     help="also record the per-wave timeline of one launch of the dominant GEMV and of the step's "
                          "smaller B = 1 GEMVs (j4q_gemv_trace)")
@@ -776,17 +788,22 @@ def main():
     regions = None
     if args.gemm_regions:
         regions = [gemm_regions(eng, m, var) for m, var in ((2048, "bf16"), (2048, "int8"), (512, "bf16"))]
+    resident = None
+    if args.resident:
+        resident = []
+        for name, qt, n, k, parts in STEP_SHAPES_B1:
+            rot = gemv_workload(eng, name, qt, n, k, 1, args.steps, args.warmup, parts)
+            res = gemv_workload(eng, name + "_resident", qt, n, k, 1, args.steps, args.warmup, parts, rotate_bytes=1)
+            resident.append({"workload": name, "us_per_launch_rotating": rot["us_per_launch"],
+                             "us_per_launch_resident": res["us_per_launch"],
+                             "median_us_rotating": rot["sampled"]["median_us"],
+                             "median_us_resident": res["sampled"]["median_us"]})
     timeline = None
     if args.timeline:
         khz = C.c_int()
         eng.hip.ok(eng.hip.h.hipDeviceGetAttribute(C.byref(khz), HIP_ATTR_WALL_CLOCK_RATE, 0), "hipDeviceGetAttribute")
         tpu = khz.value / 1e3
-        timeline = [summarize_timeline(*timeline_workload(eng, *w), tpu) for w in (
-            (DOMINANT, Q4K, 28672, 4096, [14336, 14336]),
-            ("q4_k_gemv_qkv_fused_b1", Q4K, 6144, 4096, [4096, 1024, 1024]),
-            ("q4_k_gemv_o_b1", Q4K, 4096, 4096, None),
-            ("q6_k_gemv_down_b1", Q6K, 4096, 14336, None),
-        )]
+        timeline = [summarize_timeline(*timeline_workload(eng, *w), tpu) for w in STEP_SHAPES_B1]
     if not args.quick:
         if "gemv" in groups:
             others.append(gemv_workload(eng, "q4_0_gemv_b1", QuantType.Q4_0, 11008, 4096, 1, args.steps, args.warmup))
@@ -848,6 +865,7 @@ def main():
         "calibration": cal,
         "timeline": timeline,
         "gemm_regions": regions,
+        "resident": resident,
         "host": host_description(),
         "device": eng.info,
     }
