@@ -295,6 +295,17 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // A workgroup barrier without __syncthreads()'s release fence: the fence would wait for every
 // LDS load in flight (vmcnt(0)), which is the ring this kernel keeps open. The empty asm
 // statements keep the compiler from moving memory accesses across it.
+// Wave priority p (0..3; s_setprio takes an immediate, so p must fold to a constant). The
+// stage loops below lower a wave's priority as it gets through a stage, so the wave of a SIMD
+// that is behind issues first and the two reach the next barrier together (A/B pairs on one
+// box, three rounds, bench with the quantizer: int8 M = 512 36.2-38.2 -> 35.5-36.9 us, M = 2048
+// 132.5-133.6 -> 129.9-131.1 us; bf16 M = 2048 97.7-102.2 -> 97.4-98.7 us, M = 512 level).
+__device__ __forceinline__ void wave_prio(int p) {
+    if (p >= 3) __builtin_amdgcn_s_setprio(3);
+    else if (p == 2) __builtin_amdgcn_s_setprio(2);
+    else if (p == 1) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -441,6 +452,7 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
                 d[j] = *reinterpret_cast<const uint16_t *>(db + wave * 256 + (bb * 16 * NJ + 16 * j + m16) * 2);
             }
         };
+        wave_prio(1);
         {
             u32x2 q0[NJ];
             uint32_t d0[NJ];
@@ -459,6 +471,7 @@ gemm_bf16_lds(QMat w, const uint16_t *__restrict__ x, float *__restrict__ y, int
             for (int t = 0; t < TM; t++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
+                    if (bb == 1 && t == 0 && j == 0) wave_prio(0);  // on to the stage's second block
                     acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[bb][t], b[bb][j], acc[t][j], 0, 0, 0);
                     if (ILV && mi % STRIDE == STRIDE - 1 && p < P) {
                         __builtin_amdgcn_sched_barrier(0);
@@ -1059,6 +1072,7 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
     auto stage = [&](const uint8_t *xb, const uint8_t *wb, const uint8_t *sb, int inext, uint8_t *xn, uint8_t *wn,
                      uint8_t *sn) __attribute__((always_inline)) {
         Ops o;
+        wave_prio(3);
         read_ops(xb, wb, sb, 0, o);
         __builtin_amdgcn_sched_barrier(0);
         load(inext, 0, xn, wn, sn);
@@ -1067,6 +1081,7 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
         __builtin_amdgcn_sched_barrier(0);
         products(o, pa);
         __builtin_amdgcn_sched_barrier(0);
+        wave_prio(2);
         read_ops(xb, wb, sb, 1, o);
         __builtin_amdgcn_sched_barrier(0);
         load(inext, 1, xn, wn, sn);
@@ -1077,8 +1092,10 @@ gemm_i8_lds(QMat w, const int8_t *__restrict__ xq, const float *__restrict__ xsc
         __builtin_amdgcn_sched_barrier(0);
         products(o, pb);
         __builtin_amdgcn_sched_barrier(0);
+        wave_prio(1);
         fold(pa.I0, pa.Pr, 0);
         __builtin_amdgcn_sched_barrier(0);
+        wave_prio(0);
         load(inext, 3, xn, wn, sn);
         __builtin_amdgcn_sched_barrier(0);
         fold(pa.I1, pa.Pr, 1);
