@@ -354,8 +354,10 @@ def decode_workload(eng: Engine, model: DecodeModel, batch: int, steps: int, war
 def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n: int = 4096, k: int = 4096,
                   qt: QuantType = QuantType.Q8_0):
     """Q8_0 prefill GEMM Y[m, n] = X[m, k] . W^T with bf16 X; the int8 variant's
-    timed call includes quantizing X (j4q_quant_matmul_into runs both kernels). With another
-    `qt` (Q4_0, Q4_K, Q6_K; bf16 variant) the same GEMM over configs[1]/[2]'s matrices."""
+    timed call includes quantizing X (j4q_quant_matmul_into runs both kernels). Variant
+    "int8q": the int8 GEMM alone on X quantized once before the region (j4q_quant_matmul_q8_into,
+    as for one X feeding several matrices); not a configs[3] line. With another `qt` (Q4_0,
+    Q4_K, Q6_K; bf16 variant) the same GEMM over configs[1]/[2]'s matrices."""
     blob_bytes = qt.byte_size_for(n * k)
     copies = max(1, math.ceil(ROTATE_BYTES / blob_bytes))
     ws = [eng.weights(qt, n, k, 0x5EED8 + 31 * i)[0] for i in range(copies)]
@@ -365,12 +367,18 @@ def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n:
     y = eng.hip.malloc(4 * m * n)
     handles = [w.handle for w in ws]
     fn = eng.lib.j4q_quant_matmul_into
-    v = N.GEMM_INT8 if variant == "int8" else N.GEMM_BF16
+    v = N.GEMM_BF16 if variant == "bf16" else N.GEMM_INT8
     s = C.c_void_p(eng.stream)
     xp, xqp, xsp, yp = C.c_void_p(x), C.c_void_p(xq), C.c_void_p(xs), C.c_void_p(y)
+    if variant == "int8q":
+        check(fn(handles[0], xp, m, v, xqp, xsp, yp, s), "gemm")  # leaves X quantized in xq / xs
+        fq = eng.lib.j4q_quant_matmul_q8_into
 
     def enqueue(i):
-        rc = fn(handles[i % copies], xp, m, v, xqp, xsp, yp, s)
+        if variant == "int8q":
+            rc = fq(handles[i % copies], xqp, xsp, m, yp, s)
+        else:
+            rc = fn(handles[i % copies], xp, m, v, xqp, xsp, yp, s)
         if rc:
             check(rc, "gemm")
 
@@ -382,7 +390,7 @@ def gemm_workload(eng: Engine, m: int, variant: str, steps: int, warmup: int, n:
     per = ms / steps
     ops = 2.0 * m * n * k
     tops = ops / (per * 1e-3) / 1e12
-    peak = INT8_PEAK_TOPS if variant == "int8" else BF16_PEAK_TFLOPS
+    peak = BF16_PEAK_TFLOPS if variant == "bf16" else INT8_PEAK_TOPS
     for w in ws:
         eng.be.release(w)
     for p in (x, xq, xs, y):
@@ -815,6 +823,9 @@ def main():
             for m in (32, 128, 512, 2048):
                 for variant in ("int8", "bf16"):
                     others.append(gemm_workload(eng, m, variant, args.steps, args.warmup))
+            # the int8 GEMM on X quantized once (one X feeding several Q8_0 matrices)
+            for m in (512, 2048):
+                others.append(gemm_workload(eng, m, "int8q", args.steps, args.warmup))
             # the prefill GEMM over the K-quant matrices of configs[2] and the Q4_0 one of configs[1]
             for qt, n, k in ((Q4K, 14336, 4096), (Q6K, 4096, 14336), (QuantType.Q4_0, 11008, 4096)):
                 for m in ((32, 512, 2048) if qt != QuantType.Q4_0 else (512,)):

@@ -203,6 +203,14 @@ int j4q_quant_matvec_into(j4q_buffer weights, const float *x_dev, const float *a
  * (hipMallocAsync / hipFreeAsync, at most 32 MiB); nothing else is allocated. */
 int j4q_quant_matmul_into(j4q_buffer weights, const uint16_t *x_dev, int64_t m, int variant, int8_t *xq_dev,
                           float *xs_dev, float *y_dev, void *stream);
+/* The int8 variant on activations already quantized (engine-local; no counterpart in the
+ * reference): xq_dev int8 [m, cols] and xs_dev fp32 [m, cols/32] as j4q_quantize_act makes
+ * them, and as j4q_quant_matmul_into's int8 variant leaves them in its xq/xs workspace, so
+ * one X feeding several Q8_0 matrices is quantized once. Q8_0 weights only; y_dev fp32
+ * [m, rows]; every pointer 16-byte aligned. Bit for bit the int8 variant's result for the
+ * X those activations came from. */
+int j4q_quant_matmul_q8_into(j4q_buffer weights, const int8_t *xq_dev, const float *xs_dev, int64_t m,
+                             float *y_dev, void *stream);
 
 /* The prefill GEMM for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the

@@ -140,6 +140,7 @@ SIGNATURES = {
     "j4q_quant_matvec_into": [_buf, _vp, _vp, _vp, _i64, _vp],
     "j4q_quant_matmul_into": [_buf, _vp, _i64, C.c_int, _vp, _vp, _vp, _vp],
     "j4q_quant_matmul_noalloc": [_buf, _vp, _i64, C.c_int, _vp, _vp],
+    "j4q_quant_matmul_q8_into": [_buf, _vp, _vp, _i64, _vp, _vp],
     "j4q_synth_quant_host": [C.c_int, _u64, _i64, _i64, _vp, _u64],
     "j4q_synth_quant_device": [C.c_int, _u64, _i64, _i64, _vp, _u64, _vp],
     "j4q_synth_f32_host": [_u64, _i64, _vp],

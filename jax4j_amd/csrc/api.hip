@@ -900,6 +900,22 @@ int j4q_quant_matmul_into(j4q_buffer wh, const uint16_t *x, int64_t m, int varia
     return J4Q_OK;
 }
 
+int j4q_quant_matmul_q8_into(j4q_buffer wh, const int8_t *xq, const float *xs, int64_t m, float *y, void *stream) {
+    if (!xq || !xs || !y) return fail(J4Q_EINVAL, "quantMatmul_q8_into: NULL xq, xs or y");
+    if (!aligned(xq, 16) || !aligned(xs, 16) || !aligned(y, 16))
+        return fail(J4Q_EINVAL, "quantMatmul_q8_into: pointers must be 16-byte aligned");
+    if (m <= 0) return fail(J4Q_EINVAL, "quantMatmul_q8_into: m must be positive");
+    std::lock_guard<std::mutex> lk(g_mu);
+    Buf *w;
+    int rc;
+    if ((rc = get_buf(wh, J4Q_KIND_QUANT, "quantMatmul_q8_into", &w))) return rc;
+    if ((rc = check_gemm_weights(*w, J4Q_GEMM_INT8, "quantMatmul_q8_into"))) return rc;
+    if ((rc = check_gemm_size(m, w->dims[1], J4Q_GEMM_INT8, "quantMatmul_q8_into"))) return rc;
+    if ((rc = ensure_ready())) return rc;
+    HIP_TRY("quantMatmul_q8_into", j4q::launch_gemm_q8_int8(qmat_of(*w), xq, xs, y, m, pick_stream(stream)));
+    return J4Q_OK;
+}
+
 int j4q_quant_matmul_noalloc(j4q_buffer wh, const uint16_t *x, int64_t m, int variant, float *y, void *stream) {
     if (!x || !y) return fail(J4Q_EINVAL, "quantMatmul_noalloc: NULL x or y");
     if (variant != J4Q_GEMM_INT8 && variant != J4Q_GEMM_BF16)

@@ -287,6 +287,42 @@ def test_gemm_into_caller_memory_matches(backend):
     backend.release(x)
 
 
+@pytest.mark.parametrize("m,n1,n2,k", [(70, 160, 96, 512), (512, 4096, 1024, 4096)])
+def test_gemm_prequantized_reuses_one_x(backend, m, n1, n2, k):
+    """j4q_quant_matmul_q8_into on the activations j4q_quant_matmul_into's int8 variant left in
+    its workspace for one matrix equals the int8 call on a second matrix bit for bit: one X,
+    quantized once, feeding two Q8_0 matrices."""
+    note("gemm prequantized", m, n1, n2, k)
+    lib = N.load()
+    ptr = lambda h: backend.buffer_desc(h).device_ptr
+    xb = S.activations_bf16(91, m * k).reshape(m, k)
+    x = backend.upload(xb, shape=(m, k), dtype=DType.BF16)
+    w1 = backend.upload_quantized(S.quant_blocks(QuantType.Q8_0, 92, n1, k), QuantType.Q8_0, (n1, k))
+    w2 = backend.upload_quantized(S.quant_blocks(QuantType.Q8_0, 93, n2, k), QuantType.Q8_0, (n2, k))
+    xq = backend.upload(np.zeros((m, k // 4), np.float32))  # int8 [m, k]
+    xs = backend.upload(np.zeros((m, k // 32), np.float32))
+    y1 = backend.upload(np.zeros((m, n1), np.float32))
+    y2 = backend.upload(np.zeros((m, n2), np.float32))
+    rc = lib.j4q_quant_matmul_into(w1.handle, C.c_void_p(ptr(x)), m, N.GEMM_INT8, C.c_void_p(ptr(xq)),
+                                   C.c_void_p(ptr(xs)), C.c_void_p(ptr(y1)), None)
+    assert rc == N.J4Q_OK, N.last_error()
+    rc = lib.j4q_quant_matmul_q8_into(w2.handle, C.c_void_p(ptr(xq)), C.c_void_p(ptr(xs)), m, C.c_void_p(ptr(y2)), None)
+    assert rc == N.J4Q_OK, N.last_error()
+    backend.sync()
+    ref2 = backend.download(backend.quant_matmul(w2, x, "int8")).reshape(m, n2)
+    assert np.array_equal(bits(backend.download(y2).reshape(m, n2)), bits(ref2))
+    ref1 = backend.download(backend.quant_matmul(w1, x, "int8")).reshape(m, n1)
+    assert np.array_equal(bits(backend.download(y1).reshape(m, n1)), bits(ref1))
+    # the refusals: a Q4_0 matrix, NULL or misaligned pointers, m <= 0
+    w4 = backend.upload_quantized(S.quant_blocks(QuantType.Q4_0, 94, 8, k), QuantType.Q4_0, (8, k))
+    assert lib.j4q_quant_matmul_q8_into(w4.handle, C.c_void_p(ptr(xq)), C.c_void_p(ptr(xs)), m, C.c_void_p(ptr(y2)), None) == N.J4Q_EUNSUPPORTED
+    assert lib.j4q_quant_matmul_q8_into(w2.handle, None, C.c_void_p(ptr(xs)), m, C.c_void_p(ptr(y2)), None) == N.J4Q_EINVAL
+    assert lib.j4q_quant_matmul_q8_into(w2.handle, C.c_void_p(ptr(xq) + 4), C.c_void_p(ptr(xs)), m, C.c_void_p(ptr(y2)), None) == N.J4Q_EINVAL
+    assert lib.j4q_quant_matmul_q8_into(w2.handle, C.c_void_p(ptr(xq)), C.c_void_p(ptr(xs)), 0, C.c_void_p(ptr(y2)), None) == N.J4Q_EINVAL
+    for h in (x, w1, w2, w4, xq, xs, y1, y2):
+        backend.release(h)
+
+
 def test_gemm_errors(backend):
     w4 = backend.upload_quantized(S.quant_blocks(QuantType.Q4_0, 3, 8, 64), QuantType.Q4_0, (8, 64))
     x = backend.upload(S.activations_bf16(4, 2 * 64).reshape(2, 64), shape=(2, 64), dtype=DType.BF16)
