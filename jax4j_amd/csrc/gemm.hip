@@ -444,7 +444,10 @@ hipError_t launch_gemm_q8_bf16(const QMat &w, const uint16_t *x, float *y, int64
             return hipGetLastError();
         }
         if (g128 >= 192) {
-            gw::gemm_bf16_lds<128, 1, false><<<(unsigned)g128, 512, 0, s>>>(w, x, y, (int)m);
+            // the next stage's loads spread between the MFMAs here too, since the waves' priority
+            // follows their place in the stage (A/B on one box, three rounds: M = 512 31.6-32.1 ->
+            // 30.2-30.9 us; without the priority the spread did not pay at this tile)
+            gw::gemm_bf16_lds<128, 1, true><<<(unsigned)g128, 512, 0, s>>>(w, x, y, (int)m);
             return hipGetLastError();
         }
         if (g64 >= 128) {
